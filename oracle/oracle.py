@@ -1,0 +1,270 @@
+"""ctypes view of the oracle (oracle/liboracle.so) and of the reference build
+(oracle/_ref/libwelvet_ref.so).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker; the product library never
+loads this module or the libraries behind it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libwelvet_ref.so")
+
+# include/welvet/dtype.hpp:9-44 and src/core/dtype.cpp:5-43
+DTYPE_NAMES = [
+    "float64", "float32", "float16", "bfloat16", "fp8e4m3", "fp8e5m2", "int64", "int32",
+    "int16", "int8", "uint64", "uint32", "uint16", "uint8", "int4", "uint4", "fp4", "int2",
+    "uint2", "ternary", "binary", "int", "uint", "uintptr", "complex64", "complex128", "nf4",
+    "fp6", "int6", "uint6", "int5", "uint5", "int3", "uint3",
+]
+DTYPE = {name: i for i, name in enumerate(DTYPE_NAMES)}
+ACT = {"linear": -1, "relu": 0, "silu": 1, "gelu": 2, "tanh": 3, "sigmoid": 4, "leakyrelu": 5,
+       "relu2": 6}
+
+_f = C.c_float
+_d = C.c_double
+_vp = C.c_void_p
+_i = C.c_int
+_i64 = C.c_int64
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+class Oracle:
+    """The CPU restatement (plain C, -O2 -ffp-contract=off)."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = C.CDLL(path)
+        for nm, enc, dec, ct in (("f16", "or_f32_to_f16", "or_f16_to_f32", C.c_uint16),
+                                 ("bf16", "or_f32_to_bf16", "or_bf16_to_f32", C.c_uint16),
+                                 ("e4m3", "or_f32_to_e4m3", "or_e4m3_to_f32", C.c_uint8),
+                                 ("e5m2", "or_f32_to_e5m2", "or_e5m2_to_f32", C.c_uint8),
+                                 ("fp4", "or_f32_to_fp4", "or_fp4_to_f32", C.c_uint8)):
+            getattr(L, enc).argtypes = [_f]
+            getattr(L, enc).restype = ct
+            getattr(L, dec).argtypes = [ct]
+            getattr(L, dec).restype = _f
+        L.or_native_bytes.argtypes = [_i, _i64]
+        L.or_native_bytes.restype = _i64
+        L.or_pack.argtypes = [_i, _vp, _i64, _vp, C.POINTER(_f)]
+        L.or_pack.restype = _i
+        L.or_decode.argtypes = [_i, _vp, _i64, _f, _i64, _vp]
+        L.or_decode.restype = _i
+        L.or_decode_f64.argtypes = [_i, _vp, _i64, _f, _i64, _vp]
+        L.or_decode_f64.restype = _i
+        L.or_set.argtypes = [_i, _vp, _i64, _f, _i64, _i64, _f]
+        L.or_set.restype = _i
+        L.or_native_sgd.argtypes = [_i, _vp, _i64, _f, _i64, _vp, _d]
+        L.or_native_sgd.restype = _i
+        L.or_sgd_f32.argtypes = [_vp, _vp, _i64, _d]
+        L.or_sgd_f32.restype = None
+        L.or_mse.argtypes = [_vp, _vp, _i64]
+        L.or_mse.restype = _d
+        L.or_mse_grad.argtypes = [_vp, _vp, _i64, _vp]
+        L.or_mse_grad.restype = None
+        L.or_act.argtypes = [_f, _i]
+        L.or_act.restype = _f
+        L.or_act_prime.argtypes = [_f, _i]
+        L.or_act_prime.restype = _f
+        L.or_dense_forward.argtypes = [_i, _i, _i, _i, _vp, _vp, _i64, _vp, _vp, _vp]
+        L.or_dense_forward.restype = None
+        L.or_dense_backward.argtypes = [_i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+        L.or_dense_backward.restype = None
+        L.or_normalbp.argtypes = [_i, _i, _i, _i, _i, _vp, _vp, _i64, _vp, _vp, _i, _d,
+                                  _vp, _vp, _vp, _vp, _vp, _vp]
+        L.or_normalbp.restype = _i
+        L.or_dense_forward_native.argtypes = [_i, _i, _i, _i, _i, _vp, _i64, _f, _vp, _i64, _vp,
+                                              _vp, _vp, _i]
+        L.or_dense_forward_native.restype = None
+        L.or_encode_many.argtypes = [_i, _vp, _i64, _vp]
+        L.or_encode_many.restype = None
+
+    # -- codecs ---------------------------------------------------------------
+    def native_bytes(self, dtype: int, n: int) -> int:
+        return int(self.lib.or_native_bytes(dtype, n))
+
+    def pack(self, dtype: int, w: np.ndarray) -> tuple[np.ndarray, float]:
+        w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+        out = np.zeros(self.native_bytes(dtype, w.size), np.uint8)
+        s = _f()
+        st = self.lib.or_pack(dtype, _ptr(w), w.size, _ptr(out), C.byref(s))
+        if st:
+            raise ValueError(f"or_pack status {st}")
+        return out, s.value
+
+    def decode(self, dtype: int, raw: np.ndarray, scale: float, n: int) -> np.ndarray:
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        out = np.zeros(n, np.float32)
+        st = self.lib.or_decode(dtype, _ptr(raw), raw.size, scale, n, _ptr(out))
+        if st:
+            raise ValueError(f"or_decode status {st}")
+        return out
+
+    def decode_f64(self, dtype: int, raw: np.ndarray, scale: float, n: int) -> np.ndarray:
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        out = np.zeros(n, np.float64)
+        st = self.lib.or_decode_f64(dtype, _ptr(raw), raw.size, scale, n, _ptr(out))
+        if st:
+            raise ValueError(f"or_decode_f64 status {st}")
+        return out
+
+    def set(self, dtype: int, raw: np.ndarray, scale: float, i: int, n: int, v: float) -> int:
+        return int(self.lib.or_set(dtype, _ptr(raw), raw.size, scale, i, n, v))
+
+    def native_sgd(self, dtype: int, raw: np.ndarray, scale: float, n: int, dW: np.ndarray,
+                   lr: float) -> int:
+        dW = np.ascontiguousarray(dW, dtype=np.float32).ravel()
+        return int(self.lib.or_native_sgd(dtype, _ptr(raw), raw.size, scale, n, _ptr(dW), lr))
+
+    def sgd_f32(self, w: np.ndarray, dW: np.ndarray, lr: float) -> None:
+        dW = np.ascontiguousarray(dW, dtype=np.float32)
+        self.lib.or_sgd_f32(_ptr(w), _ptr(dW), w.size, lr)
+
+    def encode_many(self, kind: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size, np.uint16 if kind in (0, 1) else np.uint8)
+        self.lib.or_encode_many(kind, _ptr(x), x.size, _ptr(out))
+        return out
+
+    # -- dense ----------------------------------------------------------------
+    def act(self, v: float, act: int) -> float:
+        return self.lib.or_act(v, act)
+
+    def act_prime(self, v: float, act: int) -> float:
+        return self.lib.or_act_prime(v, act)
+
+    def mse(self, p: np.ndarray, t: np.ndarray) -> float:
+        p = np.ascontiguousarray(p, np.float32)
+        t = np.ascontiguousarray(t, np.float32)
+        return float(self.lib.or_mse(_ptr(p), _ptr(t), p.size))
+
+    def mse_grad(self, p: np.ndarray, t: np.ndarray) -> np.ndarray:
+        p = np.ascontiguousarray(p, np.float32)
+        t = np.ascontiguousarray(t, np.float32)
+        g = np.zeros(p.size, np.float32)
+        self.lib.or_mse_grad(_ptr(p), _ptr(t), p.size, _ptr(g))
+        return g.reshape(p.shape)
+
+    def forward(self, Wd: np.ndarray, x: np.ndarray, act: int, bias: np.ndarray | None = None):
+        out, inn = Wd.shape
+        batch = x.shape[0]
+        Wd = np.ascontiguousarray(Wd, np.float64)
+        x = np.ascontiguousarray(x, np.float32)
+        pre = np.zeros((batch, out), np.float32)
+        post = np.zeros((batch, out), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+        self.lib.or_dense_forward(batch, inn, out, act, _ptr(Wd), _ptr(b),
+                                  0 if b is None else b.size, _ptr(x), _ptr(pre), _ptr(post))
+        return pre, post
+
+    def backward(self, Wd: np.ndarray, x: np.ndarray, pre: np.ndarray, gy: np.ndarray, act: int):
+        out, inn = Wd.shape
+        batch = x.shape[0]
+        Wd = np.ascontiguousarray(Wd, np.float64)
+        x = np.ascontiguousarray(x, np.float32)
+        pre = np.ascontiguousarray(pre, np.float32)
+        gy = np.ascontiguousarray(gy, np.float32)
+        dpre = np.zeros((batch, out), np.float32)
+        dX = np.zeros((batch, inn), np.float32)
+        dW = np.zeros((out, inn), np.float32)
+        self.lib.or_dense_backward(batch, inn, out, act, _ptr(Wd), _ptr(x), _ptr(pre), _ptr(gy),
+                                   _ptr(dpre), _ptr(dX), _ptr(dW))
+        return dpre, dX, dW
+
+    def normalbp(self, batch, inn, out, act, dtype, W_init, x, grad_or_target, use_target, lr,
+                 bias=None):
+        W_init = np.ascontiguousarray(W_init, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        g = np.ascontiguousarray(grad_or_target, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+        r = dict(pre=np.zeros((batch, out), np.float32), post=np.zeros((batch, out), np.float32),
+                 dX=np.zeros((batch, inn), np.float32), dW=np.zeros((out, inn), np.float32),
+                 W_after=np.zeros((out, inn), np.float32))
+        loss = _d()
+        st = self.lib.or_normalbp(batch, inn, out, act, dtype, _ptr(W_init), _ptr(b),
+                                  0 if b is None else b.size, _ptr(x), _ptr(g), int(use_target),
+                                  lr, _ptr(r["pre"]), _ptr(r["post"]), _ptr(r["dX"]),
+                                  _ptr(r["dW"]), _ptr(r["W_after"]), C.byref(loss))
+        r["loss"] = loss.value
+        r["status"] = st
+        return r
+
+    def forward_native(self, dtype, raw, scale, x, out, inn, act, bias=None, threads=1):
+        raw = np.ascontiguousarray(raw, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        batch = x.shape[0]
+        pre = np.zeros((batch, out), np.float32)
+        post = np.zeros((batch, out), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+        self.lib.or_dense_forward_native(batch, inn, out, act, dtype, _ptr(raw), raw.size, scale,
+                                         _ptr(b), 0 if b is None else b.size, _ptr(x), _ptr(pre),
+                                         _ptr(post), threads)
+        return pre, post
+
+
+class Reference:
+    """The reference's own host codec compiled from its sources (oracle/_ref)."""
+
+    def __init__(self, path: str = REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        L.ref_pack.argtypes = [_i, _vp, _i, _vp, C.c_long, C.POINTER(_f)]
+        L.ref_pack.restype = C.c_long
+        L.ref_decode.argtypes = [_i, _vp, C.c_long, _f, _i, _vp]
+        L.ref_decode.restype = _i
+        L.ref_decode_f64.argtypes = [_i, _vp, C.c_long, _f, _i, _vp]
+        L.ref_decode_f64.restype = _i
+        L.ref_encode_many.argtypes = [_i, _vp, C.c_long, _vp]
+        L.ref_encode_many.restype = None
+        for nm, ct in (("f16", C.c_uint16), ("bf16", C.c_uint16), ("e4m3", C.c_uint8),
+                       ("e5m2", C.c_uint8), ("fp4", C.c_uint8)):
+            dec = getattr(L, f"ref_{nm}_to_f32")
+            dec.argtypes = [ct]
+            dec.restype = _f
+
+    def pack(self, dtype: int, w: np.ndarray) -> tuple[np.ndarray, float]:
+        w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+        cap = 16 * w.size + 16
+        out = np.zeros(cap, np.uint8)
+        s = _f()
+        n = self.lib.ref_pack(dtype, _ptr(w), w.size, _ptr(out), cap, C.byref(s))
+        if n < 0:
+            raise ValueError(f"ref_pack status {-n}")
+        return out[:n].copy(), s.value
+
+    def decode(self, dtype: int, raw: np.ndarray, scale: float, n: int) -> np.ndarray:
+        raw = np.ascontiguousarray(raw, np.uint8)
+        out = np.zeros(n, np.float32)
+        st = self.lib.ref_decode(dtype, _ptr(raw), raw.size, scale, n, _ptr(out))
+        if st:
+            raise ValueError(f"ref_decode status {st}")
+        return out
+
+    def decode_f64(self, dtype: int, raw: np.ndarray, scale: float, n: int) -> np.ndarray:
+        raw = np.ascontiguousarray(raw, np.uint8)
+        out = np.zeros(n, np.float64)
+        st = self.lib.ref_decode_f64(dtype, _ptr(raw), raw.size, scale, n, _ptr(out))
+        if st:
+            raise ValueError(f"ref_decode_f64 status {st}")
+        return out
+
+    def encode_many(self, kind: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.size, np.uint16 if kind in (0, 1) else np.uint8)
+        self.lib.ref_encode_many(kind, _ptr(x), x.size, _ptr(out))
+        return out
+
+
+def have_reference() -> bool:
+    return os.path.exists(REF_SO)
