@@ -1,0 +1,192 @@
+"""Headline benchmark: Dense forward over packed native weights, 4096 -> 11008.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one Dense forward launch (welvet_hip_dense_forward_device) over one
+batch of synthetic input already resident in HBM.  The primary line is FP8
+E4M3, batch 1: value = packed-weight bytes per step / step time (GB/s), the
+BASELINE metric.  The same run measures NF4 batch 1 and FP8 / NF4 batch 64
+(TFLOP/s) and reports them under "results".
+
+Weights are N(0, 0.02) (generated on the device, seeded), x ~ N(0, 1).  Steps
+rotate over enough distinct weight copies that the working set exceeds
+512 MB, so the 256 MB MALL cannot serve repeated launches.  Timing: HIP events
+on the stream the kernels are launched on (torch's current stream), K steps
+between them after W warm-up steps; per-launch durations come from the same
+events (one pair per launch) in a second pass.
+
+cpu_baseline: the oracle's scalar port of the reference host path (per-element
+decode switch + f64 dot, oracle/oracle.c or_dense_forward_native), one thread,
+on the same workload for a bounded number of steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "welvet.metal_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+METRIC = "Dense fwd HBM GB/s (batch 1) & TFLOP/s (batch 64), FP8/NF4 4096x11008"
+HBM_PEAK = 8000.0        # GB/s, MI355X
+FP32_MFMA_PEAK = 157.3   # TFLOP/s, MI355X dense fp32 matrix
+IN, OUT = 4096, 11008
+MALL_BYTES = 512 << 20   # rotate past 2x the 256 MB Infinity Cache
+
+
+def packed_bytes(dtype: int) -> int:
+    bits = {4: 8, 26: 4, 5: 8, 16: 4, 9: 8}[dtype]
+    scale = 4 if dtype == 26 else 0  # NF4 keeps one f32 per-tensor scale
+    return IN * OUT * bits // 8 + scale
+
+
+def run_case(torch, pywelvet, dtype: int, batch: int, steps: int, warmup: int, seed: int):
+    dev = torch.device("cuda:0")
+    wbytes = packed_bytes(dtype)
+    copies = max(2, -(-MALL_BYTES // wbytes))
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    sessions = []
+    Wf = torch.empty((OUT, IN), dtype=torch.float32, device=dev)
+    for _ in range(copies):
+        Wf.normal_(0.0, 0.02, generator=g)
+        torch.cuda.synchronize()
+        s = pywelvet.Session.__new__(pywelvet.Session)
+        s.out, s.inn, s.batch, s.dtype = OUT, IN, batch, dtype
+        h = pywelvet.C.c_void_p()
+        pywelvet.check(pywelvet.lib().welvet_hip_dense_mount_device(
+            batch, IN, OUT, -1, dtype, pywelvet.C.c_void_p(Wf.data_ptr()), None, 0,
+            pywelvet.C.byref(h)))
+        s.h = h
+        sessions.append(s)
+    del Wf
+    x = torch.empty((batch, IN), dtype=torch.float32, device=dev).normal_(0.0, 1.0, generator=g)
+    pre = torch.empty((batch, OUT), dtype=torch.float32, device=dev)
+    post = torch.empty_like(pre)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    def step(i):
+        sessions[i % copies].forward_device(x.data_ptr(), pre.data_ptr(), post.data_ptr(), sh)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    # per-launch durations from one event pair per launch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(min(steps, 200))]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in evs)
+    launch_ms = sum(per) / len(per)
+    flops = 2.0 * batch * IN * OUT
+    r = {
+        "case": f"{pywelvet.DTYPE_NAMES[dtype]}_4096x11008_b{batch}",
+        "weight_dtype": pywelvet.DTYPE_NAMES[dtype], "batch": batch, "in": IN, "out": OUT,
+        "packed_bytes": wbytes, "weight_copies": copies, "ms_per_step": ms,
+        "launch_ms_mean": launch_ms, "launch_ms_median": per[len(per) // 2],
+        "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12,
+        "hbm_gbs_per_launch": wbytes / (launch_ms * 1e-3) / 1e9,
+        "tflops_per_launch": flops / (launch_ms * 1e-3) / 1e12,
+    }
+    for s in sessions:
+        s.close()
+    return r
+
+
+def cpu_baseline(dtype: int, batch: int, seconds: float = 12.0):
+    """Oracle scalar port, one thread, on full 4096x11008 steps, bounded time."""
+    import numpy as np
+    from oracle import Oracle
+
+    O = Oracle()
+    rng = np.random.default_rng(0x5EED0002)
+    W = rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02)
+    x = rng.standard_normal((batch, IN), dtype=np.float32)
+    raw, scale = O.pack(dtype, W)
+    steps, t = 0, 0.0
+    while t < seconds and steps < 50:
+        t0 = time.perf_counter()
+        O.forward_native(dtype, raw, scale, x, OUT, IN, -1, threads=1)
+        t += time.perf_counter() - t0
+        steps += 1
+    per = t / steps
+    return {"value": packed_bytes(dtype) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{steps} full steps of {pywelvet_name(dtype)} 4096x11008 b{batch} "
+                      f"({t:.1f} s): per-element decode switch + f64 dot, 1 thread",
+            "ms_per_step": per * 1e3}
+
+
+def pywelvet_name(dtype):
+    import pywelvet
+    return pywelvet.DTYPE_NAMES[dtype]
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of cases: fp8b1,nf4b1,fp8b64,nf4b64")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import pywelvet
+
+    pywelvet.init()
+    cases = [("fp8b1", 4, 1), ("nf4b1", 26, 1), ("fp8b64", 4, 64), ("nf4b64", 26, 64)]
+    if a.only:
+        keep = set(a.only.split(","))
+        cases = [c for c in cases if c[0] in keep]
+    results = {}
+    for i, (name, dtype, batch) in enumerate(cases):
+        results[name] = run_case(torch, pywelvet, dtype, batch, a.steps, a.warmup, 0x5EED0000 + i)
+        print(f"# {name}: {results[name]['hbm_gbs']:.1f} GB/s  {results[name]['tflops']:.2f} TFLOP/s"
+              f"  {results[name]['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+    prim = results.get("fp8b1") or next(iter(results.values()))
+    if prim["batch"] == 1:
+        ach = prim["packed_bytes"] / (prim["launch_ms_mean"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK, "unit": "GB/s",
+                "frac": ach / HBM_PEAK, "traffic": None}
+    else:
+        ach = prim["tflops_per_launch"]
+        roof = {"bound": "mfma", "achieved": ach, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
+                "frac": ach / FP32_MFMA_PEAK, "traffic": None}
+    line = {
+        "metric": METRIC, "value": prim["hbm_gbs"] if prim["batch"] == 1 else prim["tflops"],
+        "unit": "GB/s" if prim["batch"] == 1 else "TFLOP/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": prim["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: W ~ N(0,0.02) encoded to the native dtype, x ~ N(0,1)",
+        "config": {"workload": f"dense_fwd_{prim['case']}", "in": IN, "out": OUT,
+                   "batch": prim["batch"], "weight_dtype": prim["weight_dtype"],
+                   "weight_copies": prim["weight_copies"], "act": "linear"},
+        "roofline": roof,
+        "results": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in results.items()},
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(prim["weight_dtype"] == "nf4" and 26 or 4, prim["batch"])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,201 @@
+"""GPU Dense parity against the oracle: forward (GEMV, MFMA GEMM and the
+element-wise route), activations with bias, backward dX/dW, MSE, and the
+NormalBP leaf including the reference's packaged known-answer test."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import pywelvet
+from oracle import ACT, DTYPE_NAMES
+from parity import assert_bit_equal, assert_close, rel_err, tol_for_k
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    pywelvet.init()
+
+
+def oracle_weights(oracle, dtype, W):
+    raw, scale = oracle.pack(dtype, W)
+    return oracle.decode_f64(dtype, raw, scale, W.size).reshape(W.shape)
+
+
+def elementwise_bound(Wd, x, rtol):
+    """|dpre| <= rtol * sum_k |w x| per output: the condition-number bound."""
+    return rtol * (np.abs(x.astype(np.float64)) @ np.abs(Wd).T) + 1e-30
+
+
+def check_forward(oracle, dtype, W, x, act=-1, bias=None, path=0):
+    pywelvet.set_forward_path(path)
+    try:
+        pre, post = pywelvet.forward(W, x, act=act, dtype=dtype, bias=bias)
+    finally:
+        pywelvet.set_forward_path(0)
+    Wd = oracle_weights(oracle, dtype, W)
+    rpre, rpost = oracle.forward(Wd, x, act, bias)
+    k = W.shape[1]
+    assert_close(pre, rpre, k, f"{DTYPE_NAMES[dtype]} pre")
+    assert_close(post, rpost, k, f"{DTYPE_NAMES[dtype]} post")
+    if bias is None:
+        d = np.abs(pre.astype(np.float64) - rpre)
+        assert np.all(d <= elementwise_bound(Wd, x, tol_for_k(k)))
+    return pre, rpre
+
+
+@pytest.mark.parametrize("dtype", range(34), ids=DTYPE_NAMES)
+@pytest.mark.parametrize("batch", [1, 3, 8, 64])
+def test_forward_all_dtypes(oracle, dtype, batch):
+    rng = np.random.default_rng(dtype * 100 + batch)
+    W = rng.normal(0, 0.5, (96, 256)).astype(np.float32)
+    x = rng.normal(0, 1, (batch, 256)).astype(np.float32)
+    check_forward(oracle, dtype, W, x)
+
+
+@pytest.mark.parametrize("dtype", [1, 4, 9, 14, 26, 28, 0, 25])
+@pytest.mark.parametrize("path", [1, 2, 3])
+def test_forward_each_route(oracle, dtype, path):
+    rng = np.random.default_rng(7 + dtype)
+    W = rng.normal(0, 0.1, (70, 320)).astype(np.float32)
+    x = rng.normal(0, 1, (2 if path == 1 else 5, 320)).astype(np.float32)
+    check_forward(oracle, dtype, W, x, path=path)
+
+
+@pytest.mark.parametrize("dtype", [1, 2, 4, 9, 16, 26, 27, 33])
+def test_forward_ragged_shapes(oracle, dtype):
+    """Columns that are not a whole number of chunks take the element-wise route."""
+    rng = np.random.default_rng(11)
+    for out, inn, batch in ((5, 97, 1), (1, 1, 1), (3, 33, 7), (17, 250, 2)):
+        W = rng.normal(0, 0.3, (out, inn)).astype(np.float32)
+        x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+        check_forward(oracle, dtype, W, x)
+
+
+@pytest.mark.parametrize("act", list(ACT.values()) + [42], ids=list(ACT) + ["unknown"])
+def test_activations_with_bias(oracle, act):
+    rng = np.random.default_rng(5)
+    W = rng.normal(0, 0.2, (64, 128)).astype(np.float32)
+    x = rng.normal(0, 2, (4, 128)).astype(np.float32)
+    bias = rng.normal(0, 1, 40)  # shorter than out: bias only for o < 40
+    for batch in (1, 4, 9):
+        xb = np.resize(x, (batch, 128)).astype(np.float32)
+        check_forward(oracle, 1, W, xb, act=act, bias=bias)
+        check_forward(oracle, 26, W, xb, act=act, bias=bias)
+
+
+@pytest.mark.parametrize("dtype,batch", [(4, 1), (26, 1), (4, 64), (26, 64), (16, 8), (5, 32)])
+def test_forward_headline_shapes(oracle, dtype, batch):
+    """4096 -> 11008 and 11008 -> 4096 (the LLM-MLP pair) with N(0, 0.02) weights."""
+    rng = np.random.default_rng(0x5EED0003 + batch)
+    for out, inn in ((11008, 4096), (4096, 11008)):
+        W = rng.normal(0, 0.02, (out, inn)).astype(np.float32)
+        x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+        check_forward(oracle, dtype, W, x)
+
+
+def test_session_reuse(oracle):
+    rng = np.random.default_rng(3)
+    W = rng.normal(0, 0.02, (300, 512)).astype(np.float32)
+    Wd = oracle_weights(oracle, 4, W)
+    with pywelvet.Session(W, batch=2, act=3, dtype=4) as s:
+        for i in range(3):
+            x = rng.normal(0, 1, (2, 512)).astype(np.float32)
+            pre, post = s.execute(x)
+            rpre, rpost = oracle.forward(Wd, x, 3)
+            assert_close(post, rpost, 512, f"iter {i}")
+
+
+@pytest.mark.parametrize("dtype", [1, 0, 4, 9, 26, 14, 12, 27, 20])
+@pytest.mark.parametrize("batch", [1, 2, 5, 40])
+def test_backward(oracle, dtype, batch):
+    """dX within tolerance of the f64 contract; dW bit-identical (sequential
+    fmaf over the batch, welvet_dense.metal:155-178)."""
+    rng = np.random.default_rng(dtype + 31 * batch)
+    out, inn = 160, 256
+    W = rng.normal(0, 0.3, (out, inn)).astype(np.float32)
+    x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+    gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    pre = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    for act in (-1, 0, 3):
+        with pywelvet.Session(W, batch=batch, act=act, dtype=dtype) as s:
+            dX, dW = s.backward(x, pre, gy)
+        Wd = oracle_weights(oracle, dtype, W)
+        dpre, rdX, rdW = oracle.backward(Wd, x, pre, gy, act)
+        assert_close(dX, rdX, out, f"dX act={act}")
+        assert_bit_equal(dW, rdW, f"dW act={act}")
+
+
+def test_backward_ragged(oracle):
+    rng = np.random.default_rng(9)
+    W = rng.normal(0, 0.3, (13, 45)).astype(np.float32)
+    x = rng.normal(0, 1, (3, 45)).astype(np.float32)
+    gy = rng.normal(0, 1, (3, 13)).astype(np.float32)
+    pre = rng.normal(0, 1, (3, 13)).astype(np.float32)
+    for dtype in (1, 9, 26, 32):
+        with pywelvet.Session(W, batch=3, act=1, dtype=dtype) as s:
+            dX, dW = s.backward(x, pre, gy)
+        _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, 1)
+        assert_close(dX, rdX, 13)
+        assert_bit_equal(dW, rdW, "dW")
+
+
+def test_mse(oracle):
+    rng = np.random.default_rng(4)
+    for n in (1, 2, 1000, 262144 + 7):
+        p = rng.normal(0, 1, n).astype(np.float32)
+        t = rng.normal(0, 1, n).astype(np.float32)
+        loss, g = pywelvet.mse(p, t)
+        rl = oracle.mse(p, t)
+        assert abs(loss - rl) <= 1e-12 * max(1.0, abs(rl))
+        assert_bit_equal(g, oracle.mse_grad(p, t), "mse grad")
+
+
+def test_release_smoke_kat(golden_dir):
+    """scripts/release_smoke.py:45-55 through the C ABI."""
+    k = json.load(open(os.path.join(golden_dir, "release_kat.json")))
+    W = np.array(k["W_init"], np.float32).reshape(2, 2)
+    x = np.array(k["x"], np.float32).reshape(1, 2)
+    pre, post = pywelvet.forward(W, x, act=-1, dtype=1)
+    assert list(post.ravel()) == k["expect_post"]
+    r = pywelvet.normalbp(W, x, np.array(k["target"], np.float32).reshape(1, 2), 1, k["lr"])
+    assert abs(r["loss"] - k["expect_loss"]) < k["tolerance"]
+    assert np.all(np.abs(r["W_after"].ravel() - np.array(k["expect_W_after"])) < k["tolerance"])
+
+
+@pytest.mark.parametrize("dtype", [1, 0, 2, 3, 4, 5, 9, 13, 14, 16, 26, 19, 28, 7])
+def test_normalbp_matches_oracle(oracle, dtype):
+    rng = np.random.default_rng(77 + dtype)
+    for batch, out, inn, act, use_target, lr in ((1, 64, 128, 3, 1, 1e-2), (6, 40, 96, 0, 0, 0.1),
+                                                 (3, 24, 97, 2, 1, 0.0)):
+        W = rng.normal(0, 0.3, (out, inn)).astype(np.float32)
+        x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+        t = rng.normal(0, 1, (batch, out)).astype(np.float32)
+        bias = rng.normal(0, 0.1, out)
+        r = pywelvet.normalbp(W, x, t, use_target, lr, act=act, dtype=dtype, bias=bias)
+        o = oracle.normalbp(batch, inn, out, act, dtype, W, x, t, use_target, lr, bias=bias)
+        assert o["status"] == 0
+        for key in ("pre", "post", "dX", "dW"):
+            assert rel_err(r[key], o[key]) <= 1e-5, (key, rel_err(r[key], o[key]))
+        assert abs(r["loss"] - o["loss"]) <= 1e-5 * max(1.0, abs(o["loss"]))
+        # W_after: decode of the re-encoded store; tiny dW differences may move
+        # a value across one quantisation boundary, never further
+        diff = np.abs(r["W_after"].astype(np.float64) - o["W_after"])
+        step = np.max(np.abs(np.diff(np.unique(o["W_after"])))) if np.unique(o["W_after"]).size > 1 else 0
+        assert np.mean(diff > 0) <= 0.01 and (diff.max() <= step + 1e-6 or diff.max() <= 1e-5)
+
+
+def test_normalbp_error_codes():
+    W = np.ones((2, 2), np.float32)
+    x = np.ones((1, 2), np.float32)
+    g = np.array([[np.inf, 0]], np.float32)
+    r = pywelvet.normalbp(W, x, g, 0, 0.1, dtype=9, status=True)
+    assert r["status"].code == 1  # nonfinite gradient on the native path
+    r = pywelvet.normalbp(W, x, g, 0, 0.1, dtype=1, status=True)
+    assert r["status"].code == 2  # Float32 path: training.mm:122-124
+    r = pywelvet.normalbp(W, x, np.zeros((1, 2), np.float32), 0, float("inf"), dtype=9, status=True)
+    assert r["status"].code == 1
+    r = pywelvet.normalbp(W, x, np.zeros((1, 2), np.float32), 1, 0.0, dtype=9)
+    assert r["loss"] >= 0

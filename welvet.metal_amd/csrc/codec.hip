@@ -1,0 +1,328 @@
+// codec.hip — device encode (pack with fresh per-tensor statistics), decode
+// (export_f32), decode tables, and the SGD update with fixed-scale re-encode.
+//
+// These replace the reference's host pack_native / weight_at loops
+// (native_codec.cpp:189-813) and its single-thread op_native_sgd
+// (ops_storage.metal:924-958) with one-thread-per-unit HBM-streaming kernels.
+// A unit is the smallest group of elements that owns whole bytes, so no two
+// threads ever write the same byte.
+#include "codec.hpp"
+#include "kernels.hpp"
+
+namespace wh {
+namespace {
+
+constexpr int kThreads = 256;
+
+inline int grid_for(int64_t units) {
+  int64_t g = (units + kThreads - 1) / kThreads;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
+}
+
+// Order-preserving map of a non-NaN float to uint32 with -0 folded onto +0,
+// so that equal values compare equal and the element index breaks ties.
+__device__ inline uint32_t sortable(float v) {
+  const uint32_t u = f2u(v == 0.0f ? 0.0f : v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// abs_max (native_codec.cpp:22-30) and min_max (:32-40) in one pass.  The
+// sequential min/max keep the first element that attains the extreme value;
+// the (value, index) keys reproduce that, including the sign of a zero.
+__global__ void __launch_bounds__(kThreads) stats_kernel(const float *__restrict__ w, int64_t n,
+                                                         Stats *acc) {
+  float am = 0.0f;
+  uint64_t kmin = ~0ull, kmax = 0ull;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const float v = w[i];
+    const float a = fabsf(v);
+    if (a > am) am = a;
+    if (v == v) {
+      const uint64_t key = (uint64_t)sortable(v) << 32;
+      const uint64_t lo = key | (uint32_t)i, hi = key | (0xffffffffu - (uint32_t)i);
+      kmin = lo < kmin ? lo : kmin;
+      kmax = hi > kmax ? hi : kmax;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(am, off);
+    am = o > am ? o : am;
+    const uint64_t a = __shfl_xor(kmin, off), b = __shfl_xor(kmax, off);
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(&acc->absmax_bits, f2u(am));  // non-negative: bit order == value order
+    atomicMin(&acc->minkey, (unsigned long long)kmin);
+    atomicMax(&acc->maxkey, (unsigned long long)kmax);
+  }
+}
+
+__global__ void stats_init_kernel(Stats *acc) {
+  acc->absmax_bits = 0;
+  acc->minkey = ~0ull;
+  acc->maxkey = 0ull;
+}
+
+// Per-dtype scale rules of pack_native (native_codec.cpp:148-560).
+template <int DT>
+__global__ void finalize_kernel(const float *__restrict__ w, const Stats *acc, Meta *meta) {
+  const float absmax = u2f(acc->absmax_bits);
+  float mn, mx;
+  if (w[0] != w[0]) {
+    mn = mx = w[0];  // the sequential scan never leaves a NaN first element
+  } else {
+    mn = w[(uint32_t)acc->minkey];
+    mx = w[0xffffffffu - (uint32_t)acc->maxkey];
+  }
+  Meta m{1.0f, 1.0f, 0.0f, 0.0f};
+  if constexpr (DT == kInt64 || DT == kInt || DT == kInt32 || DT == kInt16) {
+    float s = absmax;
+    if (s == 0) s = 1;
+    m.s = s;
+    m.scale = s / (DT == kInt32 ? 2147483647.0f : (DT == kInt16 ? 32767.0f : 1e6f));
+  } else if constexpr (DT == kInt8 || DT == kInt4 || DT == kInt6 || DT == kFP6 || DT == kInt5 ||
+                       DT == kInt3) {
+    constexpr int bits = dtype_bits(DT);
+    float s = absmax / (float)((1 << (bits - 1)) - 1);
+    if (s == 0) s = 1;
+    m.s = m.scale = s;
+  } else if constexpr (DT == kInt2 || DT == kTernary || DT == kBinary || DT == kNF4) {
+    float s = absmax;
+    if (s == 0) s = 1;
+    m.s = m.scale = s;
+  } else if constexpr (dtype_has_min(DT)) {
+    float span = mx - mn;
+    if (span == 0) span = 1;
+    float k;
+    if constexpr (DT == kUint8) k = 255.0f;
+    else if constexpr (DT == kUint16) k = 65535.0f;
+    else if constexpr (DT == kUint32) k = 4294967296.0f;  // float(4294967295u)
+    else if constexpr (DT == kUint2) k = 3.0f;
+    else if constexpr (DT == kUint64 || DT == kUint || DT == kUintptr) k = 1e15f;
+    else k = (float)((1 << dtype_bits(DT)) - 1);
+    m.s = span;
+    m.minv = mn;
+    m.scale = span / k;
+  }
+  *meta = m;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) pack_kernel(const float *__restrict__ w, int64_t n,
+                                                        uint8_t *__restrict__ body,
+                                                        const Meta *__restrict__ meta) {
+  constexpr int bits = dtype_bits(DT);
+  constexpr int U = unit_elems<DT>();
+  const Meta m = *meta;
+  const int64_t units = (n + U - 1) / U;
+  for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < units;
+       u += (int64_t)gridDim.x * kThreads) {
+    if constexpr (bits >= 8) {
+      const uint64_t c = pack_code<DT>(w[u], m);
+      if constexpr (bits == 8) body[u] = (uint8_t)c;
+      else if constexpr (bits == 16) ((uint16_t *)body)[u] = (uint16_t)c;
+      else if constexpr (bits == 32) ((uint32_t *)body)[u] = (uint32_t)c;
+      else if constexpr (bits == 64) {
+        ((uint32_t *)body)[2 * u] = (uint32_t)c;
+        ((uint32_t *)body)[2 * u + 1] = (uint32_t)(c >> 32);
+      } else {
+        uint32_t *p = (uint32_t *)body + 4 * u;
+        p[0] = (uint32_t)c;
+        p[1] = (uint32_t)(c >> 32);
+        p[2] = 0;
+        p[3] = 0;
+      }
+    } else {
+      uint64_t acc = 0;
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int64_t i = u * U + j;
+        if (i < n) acc |= pack_code<DT>(w[i], m) << (j * bits);
+      }
+      constexpr int ubytes = U * bits / 8;
+#pragma unroll
+      for (int b = 0; b < ubytes; ++b) body[u * ubytes + b] = (uint8_t)(acc >> (8 * b));
+    }
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) decode_kernel(const uint8_t *__restrict__ body, int64_t n,
+                                                          float scale, float minv,
+                                                          float *__restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    out[i] = dec_code<DT>(load_code<DT>(body, i), scale, minv);
+}
+
+template <int DT>
+__global__ void lut_kernel(float scale, float minv, float *lut) {
+  const int c = threadIdx.x;
+  if (c < (1 << dtype_bits(DT))) lut[c] = dec_code<DT>((uint64_t)c, scale, minv);
+}
+
+// op_native_sgd ops_storage.metal:924-958 with the f64 contract: each element
+// becomes fl32(old - lr*g) re-encoded with the stored scale/min; element 0 is
+// first decoded and re-encoded once (the reference's probe, :941-945).
+template <int DT>
+__device__ inline float sgd_value(uint64_t code, int64_t i, float g, double lr, float scale, float minv) {
+  float old = dec_code<DT>(code, scale, minv);
+  if (i == 0) old = dec_code<DT>(fix_code<DT>(old, scale, minv), scale, minv);
+  return (float)((double)old - lr * (double)g);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body, int64_t n,
+                                                       const float *__restrict__ g, double lr,
+                                                       float scale, float minv) {
+  constexpr int bits = dtype_bits(DT);
+  constexpr int U = unit_elems<DT>();
+  const int64_t units = (n + U - 1) / U;
+  for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < units;
+       u += (int64_t)gridDim.x * kThreads) {
+    if constexpr (bits >= 8) {
+      const uint64_t c = fix_code<DT>(sgd_value<DT>(load_code<DT>(body, u), u, g[u], lr, scale, minv),
+                                      scale, minv);
+      constexpr int fb = fix_bytes<DT>();
+      if constexpr (fb == 1) body[u] = (uint8_t)c;
+      else if constexpr (fb == 2) ((uint16_t *)body)[u] = (uint16_t)c;
+      else if constexpr (fb == 4) ((uint32_t *)(body + u * (bits / 8)))[0] = (uint32_t)c;
+      else {
+        uint32_t *p = (uint32_t *)(body + u * (bits / 8));
+        p[0] = (uint32_t)c;
+        p[1] = (uint32_t)(c >> 32);
+      }
+    } else {
+      constexpr int ubytes = U * bits / 8;
+      uint64_t acc = 0;
+#pragma unroll
+      for (int b = 0; b < ubytes; ++b) acc |= (uint64_t)body[u * ubytes + b] << (8 * b);
+      constexpr uint64_t mask = (1ull << bits) - 1;
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int64_t i = u * U + j;
+        if (i < n) {
+          const uint64_t c = (acc >> (j * bits)) & mask;
+          const uint64_t nc = fix_code<DT>(sgd_value<DT>(c, i, g[i], lr, scale, minv), scale, minv);
+          acc = (acc & ~(mask << (j * bits))) | ((nc & mask) << (j * bits));
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < ubytes; ++b) body[u * ubytes + b] = (uint8_t)(acc >> (8 * b));
+    }
+  }
+}
+
+// Float64 storage keeps full f64: w = w - lr*g (native_codec.cpp:933-939
+// pinned to the f64 value its soft-double approximates).
+__global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ w, int64_t n,
+                                                           const float *__restrict__ g, double lr) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    w[i] = w[i] - lr * (double)g[i];
+}
+
+// welvet_sgd_f32_f64_grad welvet_dense.metal:263-281: the step is rounded to
+// f32 first, then subtracted in f32.
+__global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w, int64_t n,
+                                                           const float *__restrict__ g, double lr) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const float step = (float)(lr * (double)g[i]);
+    w[i] = w[i] - step;
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) nonfinite_kernel(const float *__restrict__ g, int64_t n,
+                                                             int *flag) {
+  int bad = 0;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    bad |= !isfinite(g[i]);
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+}  // namespace
+
+#define WH_DTYPE_SWITCH(dt, F)                                                                    \
+  switch (dt) {                                                                                   \
+  case kFloat64: F(kFloat64); case kFloat32: F(kFloat32); case kFloat16: F(kFloat16);             \
+  case kBFloat16: F(kBFloat16); case kFP8E4M3: F(kFP8E4M3); case kFP8E5M2: F(kFP8E5M2);           \
+  case kInt64: F(kInt64); case kInt32: F(kInt32); case kInt16: F(kInt16); case kInt8: F(kInt8);   \
+  case kUint64: F(kUint64); case kUint32: F(kUint32); case kUint16: F(kUint16);                   \
+  case kUint8: F(kUint8); case kInt4: F(kInt4); case kUint4: F(kUint4); case kFP4: F(kFP4);       \
+  case kInt2: F(kInt2); case kUint2: F(kUint2); case kTernary: F(kTernary);                       \
+  case kBinary: F(kBinary); case kInt: F(kInt); case kUint: F(kUint); case kUintptr: F(kUintptr); \
+  case kComplex64: F(kComplex64); case kComplex128: F(kComplex128); case kNF4: F(kNF4);           \
+  case kFP6: F(kFP6); case kInt6: F(kInt6); case kUint6: F(kUint6); case kInt5: F(kInt5);         \
+  case kUint5: F(kUint5); case kInt3: F(kInt3); case kUint3: F(kUint3);                           \
+  default: return hipErrorInvalidValue;                                                           \
+  }
+
+hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta *meta, Stats *stats,
+                         hipStream_t s) {
+  if (n <= 0) return hipErrorInvalidValue;
+  stats_init_kernel<<<1, 1, 0, s>>>(stats);
+  stats_kernel<<<grid_for(n / 4 + 1), kThreads, 0, s>>>(w, n, stats);
+#define WH_ENC(D)                                                                      \
+  finalize_kernel<D><<<1, 1, 0, s>>>(w, stats, meta);                                  \
+  pack_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
+      w, n, body, meta);                                                               \
+  return hipGetLastError();
+  WH_DTYPE_SWITCH(dt, WH_ENC)
+#undef WH_ENC
+}
+
+hipError_t launch_decode(int dt, const uint8_t *body, int64_t n, float scale, float minv, float *out,
+                         hipStream_t s) {
+#define WH_DEC(D)                                                                    \
+  decode_kernel<D><<<grid_for(n), kThreads, 0, s>>>(body, n, scale, minv, out);      \
+  return hipGetLastError();
+  WH_DTYPE_SWITCH(dt, WH_DEC)
+#undef WH_DEC
+}
+
+hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s) {
+  if (!dtype_lut(dt) || dt == kFloat32) return hipSuccess;
+#define WH_LUT(D)                                             \
+  if constexpr (dtype_bits(D) <= 8) {                          \
+    lut_kernel<D><<<1, 256, 0, s>>>(scale, minv, lut);         \
+    return hipGetLastError();                                 \
+  } else {                                                    \
+    return hipSuccess;                                        \
+  }
+  WH_DTYPE_SWITCH(dt, WH_LUT)
+#undef WH_LUT
+}
+
+hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double lr, float scale,
+                      float minv, hipStream_t s) {
+  if (dt == kFloat32) {
+    sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr);
+    return hipGetLastError();
+  }
+  if (dt == kFloat64) {
+    sgd_f64_kernel<<<grid_for(n), kThreads, 0, s>>>((double *)body, n, g, lr);
+    return hipGetLastError();
+  }
+#define WH_SGD(D)                                                                           \
+  if constexpr (D != kFloat32 && D != kFloat64) {                                           \
+    sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
+        body, n, g, lr, scale, minv);                                                       \
+    return hipGetLastError();                                                               \
+  } else {                                                                                  \
+    return hipErrorInvalidValue;                                                            \
+  }
+  WH_DTYPE_SWITCH(dt, WH_SGD)
+#undef WH_SGD
+}
+
+hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, hipStream_t s) {
+  nonfinite_kernel<<<grid_for(n / 4 + 1), kThreads, 0, s>>>(g, n, flag);
+  return hipGetLastError();
+}
+
+}  // namespace wh

@@ -1,0 +1,64 @@
+// kernels.hpp — host-side launch interface of the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wh {
+
+struct Meta;
+
+// Device scratch of the statistics pass (absmax, first min, first max).
+struct Stats {
+  unsigned int absmax_bits;
+  unsigned int pad;
+  unsigned long long minkey;
+  unsigned long long maxkey;
+};
+
+// Resident weight matrix: rows = out, cols = in (native_codec.cpp:112-136
+// bitstream order, header split off into minv).
+struct DevStore {
+  int dtype;
+  int rows;
+  int cols;
+  float scale;
+  float minv;
+  const uint8_t *body;
+  const float *lut;  // 2^bits decoded values for formats of <= 8 bits
+};
+
+// ---- codec.hip
+hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta *meta, Stats *stats,
+                         hipStream_t s);
+hipError_t launch_decode(int dt, const uint8_t *body, int64_t n, float scale, float minv, float *out,
+                         hipStream_t s);
+hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s);
+hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double lr, float scale,
+                      float minv, hipStream_t s);
+hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, hipStream_t s);
+
+// ---- dense.hip
+// Bytes of workspace the forward / backward launches below need.
+size_t forward_workspace_bytes(const DevStore &w, int batch);
+size_t backward_workspace_bytes(const DevStore &w, int batch);
+
+// pre/post [batch][rows] = act(x[batch][cols] . W^T (+ bias)).
+hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
+                          int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
+                          hipStream_t s);
+// dpre = gy * act'(pre); dX = dpre . W; dW = sum_b dpre^T x (sequential FMA);
+// flag |= 1 when dW holds a non-finite value.
+hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
+                           const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
+                           void *ws, size_t ws_bytes, hipStream_t s);
+// loss = sum (p - t)^2 / n (f64);  grad = fl32(2 (p - t) / n).
+hipError_t launch_mse(const float *pred, const float *target, int64_t n, double *loss, float *grad,
+                      void *ws, size_t ws_bytes, hipStream_t s);
+size_t mse_workspace_bytes(int64_t n);
+
+// Kernel-selection knobs, exposed for sweeps: forward path for a batch
+// (0 = auto, 1 = GEMV, 2 = MFMA GEMM, 3 = generic element-wise).
+void set_forward_path(int path);
+
+}  // namespace wh

@@ -1,0 +1,247 @@
+"""ctypes binding of libwelvet_hip.so (include/welvet_c.h).
+
+The argument lists follow the reference's own ctypes use of the same ABI
+(scripts/release_smoke.py:38-44).  This module is the host-side mirror used by
+the tests and bench.py; it loads only the HIP library and raises when the
+library is missing, so nothing here can fall back to a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libwelvet_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "welvet_c.h")
+
+# include/welvet/dtype.hpp:9-44
+DTYPE_NAMES = [
+    "float64", "float32", "float16", "bfloat16", "fp8e4m3", "fp8e5m2", "int64", "int32",
+    "int16", "int8", "uint64", "uint32", "uint16", "uint8", "int4", "uint4", "fp4", "int2",
+    "uint2", "ternary", "binary", "int", "uint", "uintptr", "complex64", "complex128", "nf4",
+    "fp6", "int6", "uint6", "int5", "uint5", "int3", "uint3",
+]
+DTYPE = {n: i for i, n in enumerate(DTYPE_NAMES)}
+ACT = {"linear": -1, "relu": 0, "silu": 1, "gelu": 2, "tanh": 3, "sigmoid": 4, "leakyrelu": 5,
+       "relu2": 6}
+
+
+class Status(C.Structure):
+    _fields_ = [("code", C.c_int32), ("message", C.c_char * 256)]
+
+
+class WelvetError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"welvet code={code}: {message}")
+        self.code = code
+
+
+_f = C.POINTER(C.c_float)
+_d = C.POINTER(C.c_double)
+_u8 = C.POINTER(C.c_uint8)
+_vp = C.c_void_p
+_i32 = C.c_int32
+
+
+def _fp(a):
+    return None if a is None else a.ctypes.data_as(_f)
+
+
+def _dp(a):
+    return None if a is None else a.ctypes.data_as(_d)
+
+
+_LIB = None
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} is not built: run python welvet.metal_amd/build.py")
+        L = C.CDLL(LIB_PATH)
+        L.welvet_version.restype = C.c_char_p
+        L.welvet_runtime_identity.restype = C.c_char_p
+        L.welvet_metal_init.restype = Status
+        L.welvet_metal_available.restype = _i32
+        geometry = [_i32] * 6
+        prefix = geometry + [_f, _d, C.c_size_t, _f]
+        L.welvet_dense_forward_f32.argtypes = prefix + [_f, _f]
+        L.welvet_dense_forward_f32.restype = Status
+        L.welvet_dense_normalbp_f32.argtypes = prefix + [_f, _i32, C.c_double] + [_f] * 5 + [_d]
+        L.welvet_dense_normalbp_f32.restype = Status
+        L.welvet_dense_mount.argtypes = [_i32] * 5 + [_f, _d, C.c_size_t, C.POINTER(_vp)]
+        L.welvet_dense_mount.restype = Status
+        L.welvet_dense_execute.argtypes = [_vp, _f, _f, _f]
+        L.welvet_dense_execute.restype = Status
+        L.welvet_dense_release.argtypes = [_vp]
+        L.welvet_dense_release.restype = None
+        L.welvet_hip_dense_mount_device.argtypes = [_i32] * 5 + [_vp, _d, C.c_size_t,
+                                                             C.POINTER(_vp)]
+        L.welvet_hip_dense_mount_device.restype = Status
+        L.welvet_hip_dense_forward_device.argtypes = [_vp, _vp, _vp, _vp, _vp]
+        L.welvet_hip_dense_forward_device.restype = Status
+        L.welvet_hip_dense_native.argtypes = [_vp, _u8, C.c_size_t, C.POINTER(C.c_size_t), _f]
+        L.welvet_hip_dense_native.restype = Status
+        L.welvet_hip_dense_export_f32.argtypes = [_vp, _f]
+        L.welvet_hip_dense_export_f32.restype = Status
+        L.welvet_hip_dense_backward.argtypes = [_vp, _f, _f, _f, _f, _f]
+        L.welvet_hip_dense_backward.restype = Status
+        L.welvet_hip_dense_sgd.argtypes = [_vp, _f, C.c_double]
+        L.welvet_hip_dense_sgd.restype = Status
+        L.welvet_hip_mse_f32.argtypes = [_f, _f, C.c_size_t, _d, _f]
+        L.welvet_hip_mse_f32.restype = Status
+        L.welvet_hip_set_forward_path.argtypes = [_i32]
+        L.welvet_hip_set_forward_path.restype = None
+        _LIB = L
+    return _LIB
+
+
+def check(st: Status) -> None:
+    if st.code:
+        raise WelvetError(st.code, st.message.decode(errors="replace"))
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def version() -> str:
+    return lib().welvet_version().decode()
+
+
+def identity() -> str:
+    return lib().welvet_runtime_identity().decode()
+
+
+def available() -> bool:
+    return bool(lib().welvet_metal_available())
+
+
+def init() -> None:
+    check(lib().welvet_metal_init())
+
+
+def set_forward_path(path: int) -> None:
+    lib().welvet_hip_set_forward_path(path)
+
+
+def forward(W, x, act=-1, dtype=1, bias=None, status=False):
+    """welvet_dense_forward_f32: W [out][in] f32, x [batch][in] -> (pre, post)."""
+    W = _f32(W)
+    x = _f32(x)
+    out, inn = W.shape
+    batch = x.shape[0]
+    b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+    pre = np.zeros((batch, out), np.float32)
+    post = np.zeros((batch, out), np.float32)
+    st = lib().welvet_dense_forward_f32(batch, inn, out, act, dtype, 0, _fp(W), _dp(b),
+                                        0 if b is None else b.size, _fp(x), _fp(pre), _fp(post))
+    if status:
+        return st, pre, post
+    check(st)
+    return pre, post
+
+
+def normalbp(W, x, grad_or_target, use_target, lr, act=-1, dtype=1, bias=None, status=False):
+    """welvet_dense_normalbp_f32 -> dict(pre, post, dX, dW, W_after, loss)."""
+    W = _f32(W)
+    x = _f32(x)
+    g = _f32(grad_or_target)
+    out, inn = W.shape
+    batch = x.shape[0]
+    b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+    r = dict(pre=np.zeros((batch, out), np.float32), post=np.zeros((batch, out), np.float32),
+             dX=np.zeros((batch, inn), np.float32), dW=np.zeros((out, inn), np.float32),
+             W_after=np.zeros((out, inn), np.float32))
+    loss = C.c_double()
+    st = lib().welvet_dense_normalbp_f32(batch, inn, out, act, dtype, 0, _fp(W), _dp(b),
+                                         0 if b is None else b.size, _fp(x), _fp(g),
+                                         int(use_target), lr, _fp(r["pre"]), _fp(r["post"]),
+                                         _fp(r["dX"]), _fp(r["dW"]), _fp(r["W_after"]),
+                                         C.byref(loss))
+    r["loss"] = loss.value
+    if status:
+        r["status"] = st
+        return r
+    check(st)
+    return r
+
+
+class Session:
+    """welvet_dense_mount / execute / release plus the welvet_hip_ extensions."""
+
+    def __init__(self, W, batch, act=-1, dtype=1, bias=None):
+        W = _f32(W)
+        self.out, self.inn = W.shape
+        self.batch = batch
+        self.dtype = dtype
+        b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+        h = _vp()
+        check(lib().welvet_dense_mount(batch, self.inn, self.out, act, dtype, _fp(W), _dp(b),
+                                       0 if b is None else b.size, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().welvet_dense_release(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def execute(self, x):
+        x = _f32(x)
+        pre = np.zeros((self.batch, self.out), np.float32)
+        post = np.zeros((self.batch, self.out), np.float32)
+        check(lib().welvet_dense_execute(self.h, _fp(x), _fp(pre), _fp(post)))
+        return pre, post
+
+    def forward_device(self, d_x: int, d_pre: int, d_post: int, stream: int | None = None):
+        check(lib().welvet_hip_dense_forward_device(self.h, d_x, d_pre, d_post, stream))
+
+    def native(self):
+        n = C.c_size_t()
+        s = C.c_float()
+        lib().welvet_hip_dense_native(self.h, None, 0, C.byref(n), C.byref(s))
+        out = np.zeros(n.value, np.uint8)
+        check(lib().welvet_hip_dense_native(self.h, out.ctypes.data_as(_u8), out.size, C.byref(n),
+                                            C.byref(s)))
+        return out, s.value
+
+    def export_f32(self):
+        out = np.zeros((self.out, self.inn), np.float32)
+        check(lib().welvet_hip_dense_export_f32(self.h, _fp(out)))
+        return out
+
+    def backward(self, x, pre, gy):
+        x, pre, gy = _f32(x), _f32(pre), _f32(gy)
+        dX = np.zeros((self.batch, self.inn), np.float32)
+        dW = np.zeros((self.out, self.inn), np.float32)
+        check(lib().welvet_hip_dense_backward(self.h, _fp(x), _fp(pre), _fp(gy), _fp(dX), _fp(dW)))
+        return dX, dW
+
+    def sgd(self, dW, lr, status=False):
+        st = lib().welvet_hip_dense_sgd(self.h, _fp(_f32(dW)), lr)
+        if status:
+            return st
+        check(st)
+
+
+def mse(pred, target):
+    p, t = _f32(pred).ravel(), _f32(target).ravel()
+    loss = C.c_double()
+    g = np.zeros(p.size, np.float32)
+    check(lib().welvet_hip_mse_f32(_fp(p), _fp(t), p.size, C.byref(loss), _fp(g)))
+    return loss.value, g
