@@ -67,7 +67,8 @@ def run_case(torch, pywelvet, dtype: int, batch: int, steps: int, warmup: int, s
     x = torch.empty((batch, IN), dtype=torch.float32, device=dev).normal_(0.0, 1.0, generator=g)
     pre = torch.empty((batch, OUT), dtype=torch.float32, device=dev)
     post = torch.empty_like(pre)
-    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)  # default priority; all launches and events on it
     sh = stream.cuda_stream
 
     def step(i):

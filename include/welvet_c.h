@@ -80,7 +80,7 @@ WELVET_API welvet_status welvet_hip_dense_mount_device(int32_t batch, int32_t in
                                                        welvet_dense_session **sess);
 
 /* Forward on device pointers (16-byte aligned) enqueued on `stream`
- * (a hipStream_t; NULL = the session's own stream); returns once enqueued. */
+ * (a hipStream_t; NULL = the HIP null stream); returns once enqueued. */
 WELVET_API welvet_status welvet_hip_dense_forward_device(welvet_dense_session *s, const float *d_x,
                                                          float *d_pre, float *d_post,
                                                          void *stream);
@@ -104,6 +104,10 @@ WELVET_API welvet_status welvet_hip_mse_f32(const float *pred, const float *targ
                                             double *loss, float *grad);
 /* Kernel route of the forward: 0 auto, 1 GEMV, 2 MFMA GEMM, 3 element-wise. */
 WELVET_API void welvet_hip_set_forward_path(int32_t path);
+/* Kernel tuning knob `key` := value, returns the previous value (-1 = unknown
+ * key).  Keys: 0 batch-1 column-stationary GEMV (1 on), 1 its rows per block
+ * (0 = default), 2 its in-lane f64 accumulation (1 on). */
+WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus
 }

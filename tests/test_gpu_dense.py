@@ -64,6 +64,39 @@ def test_forward_each_route(oracle, dtype, path):
     check_forward(oracle, dtype, W, x, path=path)
 
 
+KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24), dict(cr=1),
+         dict(cr=2), dict(cr=3), dict(cr=4), dict(reg_gemm=0), dict(gemm_occ=4),
+         dict(fast_decode=0, pair_lut=0), dict(fast_decode=1), dict(pair_lut=1),
+         dict(fast_decode=1, pair_lut=1, gemv1=0), dict(fast_decode=1, pair_lut=1, reg_gemm=0)]
+
+
+@pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
+def test_forward_kernel_variants(oracle, knobs):
+    """Every kernel variant the tuning knobs reach gives the same parity."""
+    old = {k: pywelvet.set_tuning(k, v) for k, v in knobs.items()}
+    try:
+        rng = np.random.default_rng(21)
+        for dtype in (4, 5, 9, 16, 26, 2, 1, 0, 30):
+            for out, inn, batch in ((200, 1024, 1), (96, 4096, 1), (130, 768, 40), (64, 2048, 9)):
+                W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+                x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+                check_forward(oracle, dtype, W, x)
+            W = rng.normal(0, 1.0, (96, 512)).astype(np.float32)  # exercises every E4M3 exponent
+            for batch in (1, 6):
+                x = rng.normal(0, 1, (batch, 512)).astype(np.float32)
+                check_forward(oracle, dtype, W, x)
+                gy = rng.normal(0, 1, (batch, 96)).astype(np.float32)
+                pre = rng.normal(0, 1, (batch, 96)).astype(np.float32)
+                with pywelvet.Session(W, batch=batch, act=0, dtype=dtype) as s:
+                    dX, dW = s.backward(x, pre, gy)
+                _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, 0)
+                assert_close(dX, rdX, 96, "dX")
+                assert_bit_equal(dW, rdW, "dW")
+    finally:
+        for k, v in old.items():
+            pywelvet.set_tuning(k, v)
+
+
 @pytest.mark.parametrize("dtype", [1, 2, 4, 9, 16, 26, 27, 33])
 def test_forward_ragged_shapes(oracle, dtype):
     """Columns that are not a whole number of chunks take the element-wise route."""

@@ -53,7 +53,21 @@ __global__ void __launch_bounds__(kThreads) stats_kernel(const float *__restrict
     kmin = a < kmin ? a : kmin;
     kmax = b > kmax ? b : kmax;
   }
+  __shared__ float s_am[kThreads / 64];
+  __shared__ uint64_t s_min[kThreads / 64], s_max[kThreads / 64];
+  const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
+    s_am[wave] = am;
+    s_min[wave] = kmin;
+    s_max[wave] = kmax;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // one atomic triple per block
+    for (int i = 1; i < kThreads / 64; ++i) {
+      am = s_am[i] > am ? s_am[i] : am;
+      kmin = s_min[i] < kmin ? s_min[i] : kmin;
+      kmax = s_max[i] > kmax ? s_max[i] : kmax;
+    }
     atomicMax(&acc->absmax_bits, f2u(am));  // non-negative: bit order == value order
     atomicMin(&acc->minkey, (unsigned long long)kmin);
     atomicMax(&acc->maxkey, (unsigned long long)kmax);
@@ -266,7 +280,9 @@ hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta 
                          hipStream_t s) {
   if (n <= 0) return hipErrorInvalidValue;
   stats_init_kernel<<<1, 1, 0, s>>>(stats);
-  stats_kernel<<<grid_for(n / 4 + 1), kThreads, 0, s>>>(w, n, stats);
+  int sblocks = grid_for(n / 4 + 1);
+  if (sblocks > 1024) sblocks = 1024;
+  stats_kernel<<<sblocks, kThreads, 0, s>>>(w, n, stats);
 #define WH_ENC(D)                                                                      \
   finalize_kernel<D><<<1, 1, 0, s>>>(w, stats, meta);                                  \
   pack_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \

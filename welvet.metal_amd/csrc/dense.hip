@@ -8,13 +8,13 @@
 //                         stream 16-byte chunks of each row (coalesced), x
 //                         chunks are reused across the R rows, DPP/shuffle
 //                         reduction, bias + activation fused in the store.
-//   forward, batch > 4    gemm_kernel: decoded W tiles and x tiles staged in
+//   forward, batch > 4    gemm_sk_kernel: decoded W tiles and x tiles staged in
 //                         LDS, fp32 MFMA 32x32x2, split-K with an ordered f64
 //                         reduction that applies bias + activation.
 //   dX, batch <= 2        dx_small_kernel: lanes own column chunks and walk a
 //                         segment of rows (coalesced), ordered f64 reduction
 //                         over segments.
-//   dX, batch > 2         gemm_kernel with the transposed W tile loader.
+//   dX, batch > 2         gemm_sk_kernel with the transposed W tile loader.
 //   dW                    dw_kernel: VALU sequential fmaf over the batch in
 //                         batch order, bit-identical to the reference's
 //                         outer-product accumulation (welvet_dense.metal:155-178).
@@ -31,9 +31,14 @@ namespace wh {
 namespace {
 
 // Kernel formats: dtypes sharing a body layout and decode share a kernel.
+// FL* decode through an LDS table of 2^bits exact values; FL4P is the 4-bit
+// layout read through a 256-entry table of value pairs (one read per byte);
+// FE4 / FE5 decode FP8 E4M3 / E5M2 with the hardware converts after a
+// 4-bytes-at-once fix-up to the reference's quirks; FI8 decodes Int8 by
+// integer conversion.
 enum Fmt {
   FL1, FL2, FL3, FL4, FL5, FL6, FL8, FH16, FB16, FI16, FU16, FF32, FI32, FU32, FI64, FU64, FC64,
-  FC128, FF64, kNumFmt
+  FC128, FF64, FE4, FE5, FI8, FL4P, kNumFmt
 };
 
 int fmt_of(int dt) {
@@ -64,19 +69,54 @@ int fmt_of(int dt) {
 // Chunk = the unit one lane loads: kE elements in kW dwords.
 template <int F>
 struct FI {
-  static constexpr int kBits = F == FL1 ? 1 : F == FL2 ? 2 : F == FL3 ? 3 : F == FL4 ? 4 : F == FL5 ? 5
-                             : F == FL6 ? 6 : F == FL8 ? 8 : (F == FH16 || F == FB16 || F == FI16 || F == FU16) ? 16
+  static constexpr int kBits = F == FL1 ? 1 : F == FL2 ? 2 : F == FL3 ? 3 : (F == FL4 || F == FL4P) ? 4
+                             : F == FL5 ? 5 : F == FL6 ? 6 : (F == FL8 || F == FE4 || F == FE5 || F == FI8) ? 8
+                             : (F == FH16 || F == FB16 || F == FI16 || F == FU16) ? 16
                              : (F == FF32 || F == FI32 || F == FU32) ? 32 : F == FC128 ? 128 : 64;
-  static constexpr bool kLut = kBits <= 8;
+  static constexpr bool kLut = (kBits <= 8 && F != FE4 && F != FE5 && F != FI8) || F == FL4P;
+  static constexpr bool kPair = F == FL4P;
+  // floats of LDS table: 2^bits values, or 256 value pairs
+  static constexpr int kTable = kPair ? 512 : (kLut ? (1 << kBits) : 1);
   static constexpr int kE = kBits <= 6 ? 32 : 128 / kBits;
   static constexpr int kW = kBits <= 6 ? kBits : 4;
   using Acc = std::conditional_t<F == FF64, double, float>;
 };
 
+// Fills the block's LDS table from the store's 2^bits decoded values.
+template <int F>
+__device__ inline void fill_table(float *tab, const float *lut, int tid, int nthreads) {
+  using I = FI<F>;
+  if constexpr (I::kPair) {
+    for (int b = tid; b < 256; b += nthreads) {
+      tab[2 * b] = lut[b & 15];
+      tab[2 * b + 1] = lut[b >> 4];
+    }
+  } else if constexpr (I::kLut) {
+    for (int i = tid; i < (1 << I::kBits); i += nthreads) tab[i] = lut[i];
+  }
+}
+
+// Byte-wise fix-ups for the hardware FP8 converts (4 codes per word).
+// E4M3 (float_codecs.cpp:99-117): codes with a zero exponent field decode to
+// signed zero, and 0x7f decodes to 448 = 0x7e.  E5M2 (:160-181): zero
+// exponent field -> signed zero; Inf/NaN codes match the converter.
+__device__ inline uint32_t fix_e4m3_word(uint32_t w) {
+  const uint32_t nz = ((w & 0x78787878u) + 0x78787878u) & 0x80808080u;  // exponent != 0
+  const uint32_t keep = nz | (nz - (nz >> 7)) | 0x80808080u;
+  w &= keep;
+  const uint32_t is7f = (((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u) >> 7;
+  return w ^ is7f;
+}
+__device__ inline uint32_t fix_e5m2_word(uint32_t w) {
+  const uint32_t nz = ((w & 0x7c7c7c7cu) + 0x7c7c7c7cu) & 0x80808080u;
+  return w & (nz | (nz - (nz >> 7)) | 0x80808080u);
+}
+
 int fmt_chunk_elems(int f) {
   switch (f) {
   case FL1: case FL2: case FL3: case FL4: case FL5: case FL6: return 32;
-  case FL8: return 16;
+  case FL8: case FE4: case FE5: case FI8: return 16;
+  case FL4P: return 32;
   case FH16: case FB16: case FI16: case FU16: return 8;
   case FF32: case FI32: case FU32: return 4;
   case FC128: return 1;
@@ -122,7 +162,18 @@ template <int F>
 __device__ inline typename FI<F>::Acc chunk_value(const uint32_t (&w)[FI<F>::kW], int e,
                                                   const float *lut, float scale, float minv) {
   using I = FI<F>;
-  if constexpr (I::kLut) return lut[chunk_code<I::kBits, I::kW>(w, e)];
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  if constexpr (F == FL4P) {
+    const uint32_t b = (w[e >> 3] >> (8 * ((e >> 1) & 3))) & 0xffu;
+    return lut[2 * b + (e & 1)];
+  } else if constexpr (I::kLut) return lut[chunk_code<I::kBits, I::kW>(w, e)];
+  else if constexpr (F == FE4 || F == FE5) {
+    const uint32_t q = F == FE4 ? fix_e4m3_word(w[e >> 2]) : fix_e5m2_word(w[e >> 2]);
+    f2 p;
+    if (F == FE4) p = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_fp8(q, true) : __builtin_amdgcn_cvt_pk_f32_fp8(q, false);
+    else p = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_bf8(q, true) : __builtin_amdgcn_cvt_pk_f32_bf8(q, false);
+    return (e & 1) ? p[1] : p[0];
+  } else if constexpr (F == FI8) return (float)(int8_t)(uint8_t)(w[e >> 2] >> (8 * (e & 3))) * scale;
   else if constexpr (F == FH16) {
     const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
     return (float)__builtin_bit_cast(_Float16, h);
@@ -137,6 +188,45 @@ __device__ inline typename FI<F>::Acc chunk_value(const uint32_t (&w)[FI<F>::kW]
   else if constexpr (F == FC64) return u2f(w[2 * e]);
   else if constexpr (F == FC128) return (float)u2d((uint64_t)w[0] | ((uint64_t)w[1] << 32));
   else return u2d((uint64_t)w[2 * e] | ((uint64_t)w[2 * e + 1] << 32));  // FF64
+}
+
+// All E values of a chunk, decoded before any of them is used so the table
+// reads (or converts) of a chunk are independent and issue back to back.
+template <int F>
+__device__ inline void decode_chunk(const uint32_t (&w)[FI<F>::kW], typename FI<F>::Acc (&v)[FI<F>::kE],
+                                    const float *tab, float scale, float minv) {
+  using I = FI<F>;
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  if constexpr (F == FE4 || F == FE5) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f2 lo, hi;
+      if constexpr (F == FE4) {
+        const uint32_t q = fix_e4m3_word(w[i]);
+        lo = __builtin_amdgcn_cvt_pk_f32_fp8(q, false);
+        hi = __builtin_amdgcn_cvt_pk_f32_fp8(q, true);
+      } else {
+        const uint32_t q = fix_e5m2_word(w[i]);
+        lo = __builtin_amdgcn_cvt_pk_f32_bf8(q, false);
+        hi = __builtin_amdgcn_cvt_pk_f32_bf8(q, true);
+      }
+      v[4 * i] = lo[0];
+      v[4 * i + 1] = lo[1];
+      v[4 * i + 2] = hi[0];
+      v[4 * i + 3] = hi[1];
+    }
+  } else if constexpr (F == FL4P) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t b = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+      const f2 p = ((const f2 *)tab)[b];
+      v[2 * j] = p[0];
+      v[2 * j + 1] = p[1];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < I::kE; ++e) v[e] = chunk_value<F>(w, e, tab, scale, minv);
+  }
 }
 
 template <int E>
@@ -172,6 +262,7 @@ struct GemvArgs {
   const double *bias;
   int bias_len, act;
   float *pre, *post;
+  float tab16[16];  // first 16 decoded values (the whole table of a 4-bit format)
 };
 
 // ----------------------------------------------------------------- GEMV
@@ -180,9 +271,9 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   using I = FI<F>;
   using Acc = typename I::Acc;
   constexpr int E = I::kE, W = I::kW;
-  __shared__ float lut_s[I::kLut ? (1 << I::kBits) : 1];
+  __shared__ float lut_s[I::kTable];
   if constexpr (I::kLut) {
-    for (int i = threadIdx.x; i < (1 << I::kBits); i += 256) lut_s[i] = a.lut[i];
+    fill_table<F>(lut_s, a.lut, threadIdx.x, 256);
     __syncthreads();
   }
   const int lane = threadIdx.x & 63;
@@ -230,6 +321,221 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
   }
 }
 
+// Batch-1 GEMV, column-stationary: the block's G waves split the row into
+// 64-chunk column groups (lane = one chunk, x chunk held in registers for the
+// whole kernel) and stream the block's rows in batches of 8 with all eight
+// chunk loads in flight.  Per row batch each lane forms 8 partial dots
+// (fp32 FMA over one chunk, or f64 when ACC64), a butterfly transpose-reduce
+// leaves lane l with the 64-lane sum of row (l >> 3) in f64, and the waves'
+// partials are added in wave order.
+constexpr int kRB = 8;
+
+template <int F, bool ACC64>
+__global__ void __launch_bounds__(1024) gemv1_kernel(GemvArgs a, int rows_per_block) {
+  using I = FI<F>;
+  using Acc = std::conditional_t<ACC64 || F == FF64, double, float>;
+  constexpr int E = I::kE, W = I::kW;
+  __shared__ float lut_s[I::kTable];
+  __shared__ double part[16][kRB];
+  if constexpr (I::kLut) fill_table<F>(lut_s, a.lut, threadIdx.x, blockDim.x);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, G = blockDim.x >> 6;
+  const int c = wave * 64 + lane;
+  const bool active = c < a.nchunks;
+  Acc xv[E];
+  {
+    float xf[E];
+    if (active) load_x<E>(a.x + (int64_t)c * E, xf);
+#pragma unroll
+    for (int e = 0; e < E; ++e) xv[e] = active ? (Acc)xf[e] : (Acc)0;
+  }
+  __syncthreads();
+  const int r_begin = blockIdx.x * rows_per_block;
+  const int r_end = min(a.N, r_begin + rows_per_block);
+  const uint8_t *base = a.body + (int64_t)c * (W * 4);
+  for (int r0 = r_begin; r0 < r_end; r0 += kRB) {
+    uint32_t w[kRB][W];
+#pragma unroll
+    for (int r = 0; r < kRB; ++r) {
+      if (active && r0 + r < r_end) load_words<W>(base + (int64_t)(r0 + r) * a.row_bytes, w[r]);
+      else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) w[r][i] = 0;
+      }
+    }
+    double acc[kRB];
+#pragma unroll
+    for (int r = 0; r < kRB; ++r) {
+      Acc s = 0;
+#pragma unroll
+      for (int e = 0; e < E; ++e) s = fma((Acc)chunk_value<F>(w[r], e, lut_s, a.scale, a.minv), xv[e], s);
+      acc[r] = active ? (double)s : 0.0;  // inactive lanes decode zero words: keep them out
+    }
+    // butterfly: after the xor-32/16/8 steps lane l holds row (l >> 3)
+    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1, b3 = (lane >> 3) & 1;
+    double t4[4], t2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const double keep = b5 ? acc[i + 4] : acc[i], send = b5 ? acc[i] : acc[i + 4];
+      t4[i] = keep + __shfl_xor(send, 32);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const double keep = b4 ? t4[i + 2] : t4[i], send = b4 ? t4[i] : t4[i + 2];
+      t2[i] = keep + __shfl_xor(send, 16);
+    }
+    double v = (b3 ? t2[1] : t2[0]) + __shfl_xor(b3 ? t2[0] : t2[1], 8);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 1);
+    if ((lane & 7) == 0) part[wave][lane >> 3] = v;
+    __syncthreads();
+    if (threadIdx.x < kRB && r0 + (int)threadIdx.x < r_end) {
+      double s = 0;
+      for (int g = 0; g < G; ++g) s += part[g][threadIdx.x];
+      const int row = r0 + threadIdx.x;
+      bias_act_store(s, row, a.bias, a.bias_len, a.act, a.pre, a.post, row);
+    }
+    __syncthreads();
+  }
+}
+
+// Batch-1 GEMV with every load of a lane in flight at once.  A block owns R
+// rows; its S waves split the row into column slices of 64*C chunks (lane i
+// of a wave reads chunk slice*64*C + cc*64 + i of each row: 1 KB contiguous
+// per wave per (row, cc)).  The table load is issued first, then all R*C
+// weight chunks and the C x chunks, so one memory latency covers the whole
+// wave.  Per-lane fp32 FMA over its C*E products, then an f64 butterfly
+// transpose-reduce over the R rows and an ordered f64 sum over the S slices.
+template <int F, int C, int R>
+__global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
+  using I = FI<F>;
+  using Acc = std::conditional_t<F == FF64, double, float>;
+  constexpr int E = I::kE, W = I::kW, NL = I::kTable;
+  __shared__ float lut_s[NL];
+  __shared__ double part[4][R];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float lut_v = 0.0f;
+  if constexpr (F == FL4 || F == FL4P) {
+    // the 16 decoded values come in the kernel arguments (scalar registers),
+    // so filling the LDS table waits for no vector load
+    for (int b = tid; b < (F == FL4 ? 16 : 256); b += blockDim.x) {
+      float lo = a.tab16[0], hi = a.tab16[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        lo = (b & 15) == i ? a.tab16[i] : lo;
+        hi = (b >> 4) == i ? a.tab16[i] : hi;
+      }
+      if constexpr (F == FL4) lut_s[b] = lo;
+      else {
+        lut_s[2 * b] = lo;
+        lut_s[2 * b + 1] = hi;
+      }
+    }
+    __syncthreads();
+  } else if constexpr (I::kLut) {
+    if (tid < NL) lut_v = a.lut[tid];
+  }
+  const int r0 = blockIdx.x * R;
+  const int cbase = wave * 64 * C + lane;
+  // issue order matters: vmcnt retires in order, so the table and x loads go
+  // first and row r's arithmetic waits only for loads up to row r
+  float xv[C][E];
+#pragma unroll
+  for (int cc = 0; cc < C; ++cc) {
+    const int c = cbase + cc * 64;
+    if (c < a.nchunks) load_x<E>(a.x + (int64_t)c * E, xv[cc]);
+    else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) xv[cc][e] = 0.0f;
+    }
+  }
+  uint32_t w[R][C][W];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) {
+      const int c = cbase + cc * 64;
+      if (r0 + r < a.N && c < a.nchunks)
+        load_words<W>(a.body + (int64_t)(r0 + r) * a.row_bytes + (int64_t)c * (W * 4), w[r][cc]);
+      else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) w[r][cc][i] = 0;
+      }
+    }
+  if constexpr (I::kLut && F != FL4 && F != FL4P) {
+    if (tid < NL) lut_s[tid] = lut_v;
+    for (int i = tid + blockDim.x; i < NL; i += blockDim.x) lut_s[i] = a.lut[i];
+    __syncthreads();
+  }
+  double acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    Acc s[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) {
+      if (cbase + cc * 64 < a.nchunks) {
+        Acc v[E];
+        decode_chunk<F>(w[r][cc], v, lut_s, a.scale, a.minv);
+#pragma unroll
+        for (int e = 0; e < E; ++e) s[e & 3] = fma(v[e], (Acc)xv[cc][e], s[e & 3]);
+      }
+    }
+    acc[r] = ((double)s[0] + (double)s[1]) + ((double)s[2] + (double)s[3]);
+  }
+  // butterfly over the R rows: after log2(R) exchange steps on lane bits
+  // 5, 4, ... lane l holds a partial of row (l >> (6 - log2 R)); the
+  // remaining xor steps finish the 64-lane sum.
+  double v;
+  if constexpr (R == 1) {
+    v = acc[0];
+  } else if constexpr (R == 2) {
+    const int b5 = (lane >> 5) & 1;
+    v = (b5 ? acc[1] : acc[0]) + __shfl_xor(b5 ? acc[0] : acc[1], 32);
+  } else if constexpr (R == 4) {
+    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
+    double t[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      t[i] = (b5 ? acc[i + 2] : acc[i]) + __shfl_xor(b5 ? acc[i] : acc[i + 2], 32);
+    v = (b4 ? t[1] : t[0]) + __shfl_xor(b4 ? t[0] : t[1], 16);
+  } else {  // R == 8
+    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1, b3 = (lane >> 3) & 1;
+    double t4[4], t2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      t4[i] = (b5 ? acc[i + 4] : acc[i]) + __shfl_xor(b5 ? acc[i] : acc[i + 4], 32);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      t2[i] = (b4 ? t4[i + 2] : t4[i]) + __shfl_xor(b4 ? t4[i] : t4[i + 2], 16);
+    v = (b3 ? t2[1] : t2[0]) + __shfl_xor(b3 ? t2[0] : t2[1], 8);
+  }
+  constexpr int LR = R == 1 ? 0 : (R == 2 ? 1 : (R == 4 ? 2 : 3));
+#pragma unroll
+  for (int off = 32 >> LR; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int S = blockDim.x >> 6;
+  if (S == 1) {
+    if ((lane & ((64 >> LR) - 1)) == 0) {
+      const int row = r0 + (lane >> (6 - LR));
+      if (row < a.N) bias_act_store(v, row, a.bias, a.bias_len, a.act, a.pre, a.post, row);
+    }
+    return;
+  }
+  if ((lane & ((64 >> LR) - 1)) == 0) part[wave][lane >> (6 - LR)] = v;
+  __syncthreads();
+  if (tid < R && r0 + tid < a.N) {
+    double s = 0;
+    for (int g = 0; g < S; ++g) s += part[g][tid];
+    bias_act_store(s, r0 + tid, a.bias, a.bias_len, a.act, a.pre, a.post, r0 + tid);
+  }
+}
+
+// Batch-1 GEMV, persistent and software-pipelined: a fixed number of waves
+// (a few per CU) each hold their x chunks in registers for the whole kernel
+// (one wave covers a row's C*64 chunks) and walk row groups of R rows strided
+// by the wave count.  The next group's R*C weight chunks are loaded while the
+// current group is decoded and multiplied, so HBM streams continuously and
+// the VALU work overlaps it; each group ends with a butterfly reduction whose
+// owning lanes store the rows.
 // Element-wise fallback for shapes whose rows do not start on a chunk
 // boundary: a block per output row, f64 accumulation, any batch.
 template <int DT>
@@ -257,113 +563,290 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(DevStore w, int batch
 }
 
 // ----------------------------------------------------------------- GEMM
-// C[m][n] = sum_k A[m][k] * Wop[k][n] over fp32 MFMA 32x32x2.
-//   forward: A = x [M][K], Wop[k][n] = W[n][k]   (TRANS = false)
+// C[m][n] = sum_k A[m][k] * Wop[k][n] over fp32 MFMA 32x32x2, stream-K.
+//   forward: A = x [M][K], Wop[k][n] = W[n][k]        (TRANS = false)
 //   dX:      A = dpre [M][K=rows], Wop[k][n] = W[k][n] (TRANS = true)
+// The (tile, k-stage) iteration space is cut into equal contiguous shares,
+// one per workgroup (two resident per CU), so every CU gets the same work
+// whatever the tile count.  Each share stages A and decoded W tiles in
+// double-buffered LDS (the next stage's global loads are in flight during
+// the current stage's MFMAs), writes one partial tile per tile it touches,
+// and sk_reduce_kernel adds a tile's partials in workgroup order in f64.
 struct GemmArgs {
   const uint8_t *body;
   const float *lut;
   float scale, minv;
   const float *A;
-  int M, K, N;       // product dims
+  int M, K, N;        // product dims
   int64_t row_bytes;  // bytes per stored W row
-  int stages_per_slice, nstages;
-  float *ws;          // split-K partials [slices][M][N] (unused when direct)
-  int direct;
-  const double *bias;
-  int bias_len, act;
-  float *pre, *post;  // direct forward outputs; dX writes `pre`
+  int gx, gy, nst;    // tiles along N, along M; k stages
+  int per_block, maxspan;
+  float *ws;          // [blocks][maxspan][bm][bn] partial tiles
+  int bm, bn;         // tile shape of the kernel that wrote ws
 };
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 64, kBN = 64, kBK = 32, kPad = 1;
+constexpr int kBM = 64, kBN = 64, kBK = 64, kPad = 1;
 
 template <int F, bool TRANS>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
+struct TileLoader {
   using I = FI<F>;
-  constexpr int E = I::kE, W = I::kW;
-  __shared__ float Xs[kBK][kBM + kPad];
-  __shared__ float Ws[kBK][kBN + kPad];
-  __shared__ float lut_s[I::kLut ? (1 << I::kBits) : 1];
-  if constexpr (I::kLut) {
-    for (int i = threadIdx.x; i < (1 << I::kBits); i += 256) lut_s[i] = a.lut[i];
+  static constexpr int E = I::kE, W = I::kW;
+  static constexpr int kChunks = TRANS ? kBK * (kBN / E) : kBN * (kBK / E);
+  static constexpr int kCPT = (kChunks + 255) / 256;
+  static constexpr int kA4 = kBM * kBK / 4 / 256;
+  uint32_t w[kCPT][W];
+  float av[kA4][4];
+
+  __device__ void load(const GemmArgs &a, int m0, int n0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < kCPT; ++i) {
+      const int q = tid + i * 256;
+      bool ok = q < kChunks;
+      const uint8_t *p = nullptr;
+      if constexpr (!TRANS) {
+        const int n = q % kBN, j = q / kBN, k = k0 + j * E, row = n0 + n;
+        ok = ok && row < a.N && k < a.K;
+        p = a.body + (int64_t)row * a.row_bytes + (int64_t)(k / E) * (W * 4);
+      } else {
+        const int kl = q % kBK, j = q / kBK, k = k0 + kl, col = n0 + j * E;
+        ok = ok && k < a.K && col < a.N;
+        p = a.body + (int64_t)k * a.row_bytes + (int64_t)(col / E) * (W * 4);
+      }
+      if (ok) load_words<W>(p, w[i]);
+      else {
+#pragma unroll
+        for (int j = 0; j < W; ++j) w[i][j] = 0;
+      }
+    }
+    const bool vec = (a.K & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < kA4; ++i) {
+      const int q = tid + i * 256, m = q / (kBK / 4), k = k0 + 4 * (q % (kBK / 4));
+      const int mg = m0 + m;
+      const float *src = a.A + (int64_t)mg * a.K + k;
+      if (mg < a.M && vec && k + 3 < a.K) {
+        const float4 v = *(const float4 *)src;
+        av[i][0] = v.x; av[i][1] = v.y; av[i][2] = v.z; av[i][3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) av[i][t] = (mg < a.M && k + t < a.K) ? src[t] : 0.0f;
+      }
+    }
   }
+
+  __device__ void store(float (*Xs)[kBM + kPad], float (*Ws)[kBN + kPad], const GemmArgs &a,
+                        const float *lut, int m0, int n0, int k0, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kCPT; ++i) {
+      const int q = tid + i * 256;
+      if (q >= kChunks) break;
+      if constexpr (!TRANS) {
+        const int n = q % kBN, j = q / kBN;
+        const bool ok = n0 + n < a.N && k0 + j * E < a.K;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          Ws[j * E + e][n] = ok ? (float)chunk_value<F>(w[i], e, lut, a.scale, a.minv) : 0.0f;
+      } else {
+        const int kl = q % kBK, j = q / kBK;
+        const bool ok = k0 + kl < a.K && n0 + j * E < a.N;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          Ws[kl][j * E + e] = ok ? (float)chunk_value<F>(w[i], e, lut, a.scale, a.minv) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kA4; ++i) {
+      const int q = tid + i * 256, m = q / (kBK / 4), kl = 4 * (q % (kBK / 4));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) Xs[kl + t][m] = av[i][t];
+    }
+  }
+};
+
+template <int F, bool TRANS>
+__global__ void __launch_bounds__(256, 2) gemm_sk_kernel(GemmArgs a) {
+  using I = FI<F>;
+  __shared__ float Xs[2][kBK][kBM + kPad];
+  __shared__ float Ws[2][kBK][kBN + kPad];
+  __shared__ float lut_s[I::kTable];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM, slice = blockIdx.z;
-  const int st0 = slice * a.stages_per_slice;
-  const int st1 = min(a.nstages, st0 + a.stages_per_slice);
-  floatx16 acc;
+  if constexpr (I::kLut) fill_table<F>(lut_s, a.lut, tid, 256);
+  __syncthreads();
+  const int T = a.gx * a.gy * a.nst;
+  int it = blockIdx.x * a.per_block;
+  const int it_end = min(T, it + a.per_block);
+  const int first_tile = it / a.nst;
+  TileLoader<F, TRANS> L;
+  while (it < it_end) {
+    const int t = it / a.nst, s0 = it % a.nst;
+    const int nseg = min(it_end, (t + 1) * a.nst) - it;
+    const int m0 = (t / a.gx) * kBM, n0 = (t % a.gx) * kBN;
+    floatx16 acc;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-
-  for (int st = st0; st < st1; ++st) {
-    const int k0 = st * kBK;
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    L.load(a, m0, n0, s0 * kBK, tid);
+    L.store(Xs[0], Ws[0], a, lut_s, m0, n0, s0 * kBK, tid);
     __syncthreads();
-    // W tile -> Ws[k][n] (decoded f32)
-    if constexpr (!TRANS) {
-      constexpr int CPR = (kBK + E - 1) / E;  // chunks per row in a stage
-      for (int q = tid; q < kBN * CPR; q += 256) {
-        const int n = q % kBN, j = q / kBN, k = k0 + j * E, row = n0 + n;
-        uint32_t w[W];
-        const bool ok = row < a.N && k < a.K;
-        if (ok) load_words<W>(a.body + (int64_t)row * a.row_bytes + (int64_t)(k / E) * (W * 4), w);
+    for (int s = 0; s < nseg; ++s) {
+      const int cur = s & 1;
+      const int knext = (s0 + s + 1) * kBK;
+      if (s + 1 < nseg) L.load(a, m0, n0, knext, tid);
 #pragma unroll
-        for (int e = 0; e < E; ++e)
-          if (j * E + e < kBK) Ws[j * E + e][n] = ok ? (float)chunk_value<F>(w, e, lut_s, a.scale, a.minv) : 0.0f;
+      for (int kk = 0; kk < kBK; kk += 2) {
+        const float av = Xs[cur][kk + (lane >> 5)][wm * 32 + (lane & 31)];
+        const float bv = Ws[cur][kk + (lane >> 5)][wn * 32 + (lane & 31)];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
       }
-    } else {
-      constexpr int CPR = kBN / E;  // chunks across the tile's columns
-      for (int q = tid; q < kBK * CPR; q += 256) {
-        const int kl = q % kBK, j = q / kBK, k = k0 + kl, col = n0 + j * E;
-        uint32_t w[W];
-        const bool ok = k < a.K && col < a.N;
-        if (ok) load_words<W>(a.body + (int64_t)k * a.row_bytes + (int64_t)(col / E) * (W * 4), w);
+      if (s + 1 < nseg) L.store(Xs[cur ^ 1], Ws[cur ^ 1], a, lut_s, m0, n0, knext, tid);
+      __syncthreads();
+    }
+    // D[i][j]: lane = j + 32*((i/4)%2), register = i%4 + 4*(i/8)
+    float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (kBM * kBN);
 #pragma unroll
-        for (int e = 0; e < E; ++e)
-          Ws[kl][j * E + e] = (ok && col + e < a.N) ? (float)chunk_value<F>(w, e, lut_s, a.scale, a.minv) : 0.0f;
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int m = wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      dst[m * kBN + wn * 32 + (lane & 31)] = acc[r];
     }
-    // A tile -> Xs[k][m]
-    for (int q = tid; q < kBM * kBK; q += 256) {
-      const int kl = q % kBK, m = q / kBK, k = k0 + kl;  // lanes walk k: coalesced rows of A
-      Xs[kl][m] = (m0 + m < a.M && k < a.K) ? a.A[(int64_t)(m0 + m) * a.K + k] : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < kBK; kk += 2) {
-      const float av = Xs[kk + (lane >> 5)][wm * 32 + (lane & 31)];
-      const float bv = Ws[kk + (lane >> 5)][wn * 32 + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
-    }
-  }
-  // D[i][j]: lane = j + 32*((i/4)%2), register = i%4 + 4*(i/8)
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    const int n = n0 + wn * 32 + (lane & 31);
-    if (m < a.M && n < a.N) {
-      const int64_t idx = (int64_t)m * a.N + n;
-      if (a.direct) {
-        if constexpr (TRANS) a.pre[idx] = acc[r];
-        else bias_act_store((double)acc[r], n, a.bias, a.bias_len, a.act, a.pre, a.post, idx);
-      } else {
-        a.ws[(int64_t)slice * a.M * a.N + idx] = acc[r];
-      }
-    }
+    it += nseg;
   }
 }
 
-// Ordered f64 sum of split-K / segment partials.
-__global__ void __launch_bounds__(256) reduce_fwd_kernel(const float *ws, int slices, int M, int N,
-                                                         const double *bias, int bias_len, int act,
-                                                         float *pre, float *post) {
-  const int64_t total = (int64_t)M * N;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+// Forward GEMM for formats of <= 16 bits with W decoded straight into MFMA
+// B-operand registers (no LDS round trip).  Inside a 64-deep k stage the
+// MFMA k slot h of step t stands for k = k0 + 32h + t, so lane (j, h) of a
+// wave reads 32 consecutive weights of its own row n0 + j (one to four
+// 16-byte chunks) and only the x tile goes through LDS, shared by the block's
+// four waves.  Wave w computes rows m0..m0+32*MT of output columns
+// n0+32w..n0+32w+31 (MT accumulators sharing each decoded B value); the block
+// tile is 32*MT x 128.  Stream-K over (tile, stage) like gemm_sk_kernel, with
+// the next stage's x and weight words loaded while the current MFMAs run.
+constexpr int kRegBN = 128;
+
+template <int F, int MT>
+__global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs a) {
+  using I = FI<F>;
+  constexpr int E = I::kE, W = I::kW;
+  constexpr int BM = 32 * MT;
+  constexpr int NCH = 32 / E;          // chunks per lane per stage
+  constexpr int A4 = BM * kBK / 4 / 256;  // float4 of x per thread per stage
+  __shared__ float Xs[2][kBK][BM + kPad];
+  __shared__ float lut_s[I::kTable];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  if constexpr (I::kLut) fill_table<F>(lut_s, a.lut, tid, 256);
+  __syncthreads();
+  const int T = a.gx * a.gy * a.nst;
+  int it = blockIdx.x * a.per_block;
+  const int it_end = min(T, it + a.per_block);
+  const int first_tile = it / a.nst;
+  const bool vec = (a.K & 3) == 0;
+  uint32_t wr[NCH][W];
+  float xa[A4][4];
+  auto load_stage = [&](int m0, int n0, int k0) {
+    const int row = n0 + wave * 32 + j;
+    const int kk = k0 + 32 * h;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int k = kk + c * E;
+      if (row < a.N && k < a.K)
+        load_words<W>(a.body + (int64_t)row * a.row_bytes + (int64_t)(k / E) * (W * 4), wr[c]);
+      else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) wr[c][i] = 0;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < A4; ++i) {
+      const int q = tid + i * 256, m = q / (kBK / 4), k = k0 + 4 * (q % (kBK / 4)), mg = m0 + m;
+      const float *src = a.A + (int64_t)mg * a.K + k;
+      if (mg < a.M && vec && k + 3 < a.K) {
+        const float4 v = *(const float4 *)src;
+        xa[i][0] = v.x; xa[i][1] = v.y; xa[i][2] = v.z; xa[i][3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) xa[i][t] = (mg < a.M && k + t < a.K) ? src[t] : 0.0f;
+      }
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A4; ++i) {
+      const int q = tid + i * 256, m = q / (kBK / 4), kl = 4 * (q % (kBK / 4));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) Xs[buf][kl + t][m] = xa[i][t];
+    }
+  };
+  while (it < it_end) {
+    const int t = it / a.nst, s0 = it % a.nst;
+    const int nseg = min(it_end, (t + 1) * a.nst) - it;
+    const int m0 = (t / a.gx) * BM, n0 = (t % a.gx) * kRegBN;
+    floatx16 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][i] = 0.0f;
+    load_stage(m0, n0, s0 * kBK);
+    store_x(0);
+    __syncthreads();
+    for (int s = 0; s < nseg; ++s) {
+      const int cur = s & 1;
+      const int k0 = (s0 + s) * kBK;
+      float bv[32];
+      const bool live = n0 + wave * 32 + j < a.N;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const bool ok = live && k0 + 32 * h + c * E < a.K;
+          bv[c * E + e] = ok ? (float)chunk_value<F>(wr[c], e, lut_s, a.scale, a.minv) : 0.0f;
+        }
+      if (s + 1 < nseg) load_stage(m0, n0, k0 + kBK);
+#pragma unroll
+      for (int tt = 0; tt < 32; ++tt) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const float av = Xs[cur][32 * h + tt][mt * 32 + j];
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv[tt], acc[mt], 0, 0, 0);
+        }
+      }
+      if (s + 1 < nseg) store_x(cur ^ 1);
+      __syncthreads();
+    }
+    float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * kRegBN);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        dst[m * kRegBN + wave * 32 + j] = acc[mt][r];
+      }
+    it += nseg;
+  }
+}
+
+// Sum of a tile's stream-K partials in workgroup order (f64); the forward
+// applies bias + activation, dX stores fl32 of the sum.
+template <bool FWD>
+__global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double *bias, int bias_len,
+                                                        int act, float *out, float *post) {
+  const int64_t total = (int64_t)a.M * a.N;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * 256) {
+    const int m = (int)(idx / a.N), n = (int)(idx % a.N);
+    const int ty = m / a.bm, tx = n / a.bn, t = ty * a.gx + tx;
+    const int b0 = (int)((int64_t)t * a.nst / a.per_block);
+    const int b1 = (int)(((int64_t)(t + 1) * a.nst - 1) / a.per_block);
+    const int off = (m - ty * a.bm) * a.bn + (n - tx * a.bn);
     double s = 0;
-    for (int k = 0; k < slices; ++k) s += (double)ws[(int64_t)k * total + i];
-    bias_act_store(s, (int)(i % N), bias, bias_len, act, pre, post, i);
+    for (int b = b0; b <= b1; ++b) {
+      const int slot = t - (int)((int64_t)b * a.per_block / a.nst);
+      s += (double)a.ws[((int64_t)b * a.maxspan + slot) * (a.bm * a.bn) + off];
+    }
+    if constexpr (FWD) bias_act_store(s, n, bias, bias_len, act, out, post, idx);
+    else out[idx] = (float)s;
   }
 }
 
@@ -401,9 +884,9 @@ __global__ void __launch_bounds__(256) dx_small_kernel(DxArgs a) {
   using I = FI<F>;
   using Acc = typename I::Acc;
   constexpr int E = I::kE, W = I::kW;
-  __shared__ float lut_s[I::kLut ? (1 << I::kBits) : 1];
+  __shared__ float lut_s[I::kTable];
   if constexpr (I::kLut) {
-    for (int i = threadIdx.x; i < (1 << I::kBits); i += 256) lut_s[i] = a.lut[i];
+    fill_table<F>(lut_s, a.lut, threadIdx.x, 256);
     __syncthreads();
   }
   const int c = blockIdx.x * 256 + threadIdx.x;
@@ -533,6 +1016,8 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
+// Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1};
 
 inline int blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
@@ -544,27 +1029,65 @@ bool chunk_aligned(const DevStore &w, int64_t len) {
   return f >= 0 && len % fmt_chunk_elems(f) == 0;
 }
 
+// Kernel format of a dtype under the current knobs.
+int kernel_fmt(int dt) {
+  const int f = fmt_of(dt);
+  if (g_tune[kTuneFastDecode]) {
+    if (dt == kFP8E4M3) return FE4;
+    if (dt == kFP8E5M2) return FE5;
+    if (dt == kInt8) return FI8;
+  }
+  if (f == FL4 && g_tune[kTunePairLut]) return FL4P;
+  return f;
+}
+
 int64_t row_bytes_of(const DevStore &w) {
   return (int64_t)w.cols * dtype_bits(w.dtype) / 8;
 }
 
-struct GemmPlan {
-  int slices, stages_per_slice, nstages, gx, gy;
+int num_cus() {
+  static int n = [] {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || v <= 0)
+      v = 256;
+    return v;
+  }();
+  return n;
+}
+
+struct SkPlan {
+  int gx, gy, nst, per_block, blocks, maxspan, bm, bn;
+  size_t ws_bytes;
 };
 
-GemmPlan plan_gemm(int M, int K, int N) {
-  GemmPlan p;
-  p.nstages = (K + kBK - 1) / kBK;
-  p.gx = (N + kBN - 1) / kBN;
-  p.gy = (M + kBM - 1) / kBM;
-  const int tiles = p.gx * p.gy;
-  int s = (1024 + tiles - 1) / tiles;
-  if (s > p.nstages) s = p.nstages;
-  if (s > 64) s = 64;
-  if (s < 1) s = 1;
-  p.stages_per_slice = (p.nstages + s - 1) / s;
-  p.slices = (p.nstages + p.stages_per_slice - 1) / p.stages_per_slice;
+// Stream-K split of an M x N x K product over bm x bn tiles into equal
+// shares, `occ` workgroups per CU.
+SkPlan plan_sk(int M, int K, int N, int bm = kBM, int bn = kBN, int occ = 2) {
+  SkPlan p;
+  p.bm = bm;
+  p.bn = bn;
+  p.gx = (N + bn - 1) / bn;
+  p.gy = (M + bm - 1) / bm;
+  p.nst = (K + kBK - 1) / kBK;
+  const int64_t T = (int64_t)p.gx * p.gy * p.nst;
+  const int64_t G = (int64_t)occ * num_cus();
+  p.per_block = (int)((T + G - 1) / G);
+  p.blocks = (int)((T + p.per_block - 1) / p.per_block);
+  p.maxspan = (p.per_block + p.nst - 1) / p.nst + 1;
+  p.ws_bytes = (size_t)p.blocks * p.maxspan * bm * bn * sizeof(float);
   return p;
+}
+
+bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // formats of <= 16 bits
+
+// Forward GEMM plan: the register-B kernel for <= 16-bit formats, else the
+// LDS-staged kernel.
+SkPlan plan_fwd_gemm(int f, int M, int K, int N) {
+  if (reg_gemm_ok(f) && g_tune[kTuneRegGemm] != 0) {
+    const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
+    return plan_sk(M, K, N, M <= 32 ? 32 : 64, kRegBN, occ);
+  }
+  return plan_sk(M, K, N);
 }
 
 constexpr int kDxSegRows = 32;
@@ -600,6 +1123,7 @@ hipError_t gemv_dispatch(int batch, const GemvArgs &a, hipStream_t s) {
   case FL6: F(FL6); case FL8: F(FL8); case FH16: F(FH16); case FB16: F(FB16); case FI16: F(FI16);    \
   case FU16: F(FU16); case FF32: F(FF32); case FI32: F(FI32); case FU32: F(FU32); case FI64: F(FI64); \
   case FU64: F(FU64); case FC64: F(FC64); case FC128: F(FC128); case FF64: F(FF64);                  \
+  case FE4: F(FE4); case FE5: F(FE5); case FI8: F(FI8); case FL4P: F(FL4P);                          \
   default: return hipErrorInvalidValue;                                                              \
   }
 
@@ -622,17 +1146,23 @@ hipError_t gemv_dispatch(int batch, const GemvArgs &a, hipStream_t s) {
 
 void set_forward_path(int path) { g_forward_path = path; }
 
+int set_tuning(int key, int value) {
+  if (key < 0 || key >= kNumTune) return -1;
+  const int old = g_tune[key];
+  g_tune[key] = value;
+  return old;
+}
+
 size_t forward_workspace_bytes(const DevStore &w, int batch) {
   if (fwd_route(w, batch) != 2) return 0;
-  const GemmPlan p = plan_gemm(batch, w.cols, w.rows);
-  return p.slices > 1 ? (size_t)p.slices * batch * w.rows * sizeof(float) : 0;
+  return plan_fwd_gemm(kernel_fmt(w.dtype), batch, w.cols, w.rows).ws_bytes;
 }
 
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
                           int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
                           hipStream_t s) {
   const int route = fwd_route(w, batch);
-  const int f = fmt_of(w.dtype);
+  const int f = kernel_fmt(w.dtype);
   if (route == 3 || (route == 1 && batch > 4)) {
 #define WH_GEN(D)                                                                        \
   gemv_generic_kernel<D><<<w.rows, 256, 0, s>>>(w, batch, x, bias, bias_len, act, pre, post); \
@@ -642,26 +1172,75 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   }
   if (route == 1) {
     GemvArgs a{w.body, w.lut, w.scale, w.minv, x, w.cols, w.rows, w.cols / fmt_chunk_elems(f),
-               row_bytes_of(w), bias, bias_len, act, pre, post};
+               row_bytes_of(w), bias, bias_len, act, pre, post, {}};
+    for (int i = 0; i < 16; ++i) a.tab16[i] = w.tab16[i];
+    if (batch == 1 && g_tune[kTuneGemv1] == 1) {
+      // (C, R): chunks per lane and rows per block, C*R = 8 loads per lane
+      int C = 1;
+      switch (g_tune[kTuneCR]) {
+      case 1: C = 2; break;
+      case 2: C = 4; break;
+      case 3: C = 1; break;
+      case 4: C = 8; break;
+      default:
+        while (C < 8 && (a.nchunks + 64 * C - 1) / (64 * C) > 4) C *= 2;
+      }
+      const int S = (a.nchunks + 64 * C - 1) / (64 * C);
+      if (S <= 4) {
+        const int R = 8 / C;
+        const int blocks = (a.N + R - 1) / R;
+#define WH_PF(F)                                                                         \
+  if (C == 1) gemv_pf_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a);                      \
+  else if (C == 2) gemv_pf_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a);                 \
+  else if (C == 4) gemv_pf_kernel<F, 4, 2><<<blocks, 64 * S, 0, s>>>(a);                 \
+  else gemv_pf_kernel<F, 8, 1><<<blocks, 64 * S, 0, s>>>(a);                             \
+  return hipGetLastError();
+        WH_FMT_SWITCH(f, WH_PF)
+#undef WH_PF
+      }
+    }
+    if (batch == 1 && a.nchunks <= 1024 && g_tune[kTuneGemv1] == 2) {
+      const int G = (a.nchunks + 63) / 64;
+      int rpb = g_tune[kTuneRowsPerBlock];
+      if (rpb <= 0) rpb = 16;
+      rpb = (rpb + kRB - 1) / kRB * kRB;
+      const int blocks = (a.N + rpb - 1) / rpb;
+      const bool acc64 = g_tune[kTuneAcc64] != 0;
+#define WH_GV1(F)                                                                   \
+  if (acc64) gemv1_kernel<F, true><<<blocks, 64 * G, 0, s>>>(a, rpb);               \
+  else gemv1_kernel<F, false><<<blocks, 64 * G, 0, s>>>(a, rpb);                    \
+  return hipGetLastError();
+      WH_FMT_SWITCH(f, WH_GV1)
+#undef WH_GV1
+    }
 #define WH_GV(F) return gemv_dispatch<F>(batch, a, s);
     WH_FMT_SWITCH(f, WH_GV)
 #undef WH_GV
   }
-  const GemmPlan p = plan_gemm(batch, w.cols, w.rows);
-  if (p.slices > 1 && ws_bytes < (size_t)p.slices * batch * w.rows * sizeof(float))
-    return hipErrorInvalidValue;
+  const SkPlan p = plan_fwd_gemm(f, batch, w.cols, w.rows);
+  if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
   GemmArgs a{w.body, w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
-             p.stages_per_slice, p.nstages, (float *)ws, p.slices == 1, bias, bias_len, act, pre, post};
-  dim3 grid(p.gx, p.gy, p.slices);
-#define WH_GM(F)                                      \
-  gemm_kernel<F, false><<<grid, 256, 0, s>>>(a);      \
+             p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
+  if (p.bn == kRegBN) {
+#define WH_GR(F)                                                                      \
+  if constexpr (FI<F>::kBits <= 16) {                                                 \
+    if (p.bm == 32) gemm_reg_kernel<F, 1><<<p.blocks, 256, 0, s>>>(a);                \
+    else gemm_reg_kernel<F, 2><<<p.blocks, 256, 0, s>>>(a);                           \
+  }                                                                                   \
   break;
-  WH_FMT_SWITCH(f, WH_GM)
+    WH_FMT_SWITCH(f, WH_GR)
+#undef WH_GR
+  } else {
+#define WH_GM(F)                                              \
+  gemm_sk_kernel<F, false><<<p.blocks, 256, 0, s>>>(a);      \
+  break;
+    WH_FMT_SWITCH(f, WH_GM)
 #undef WH_GM
+  }
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.slices == 1) return e;
-  reduce_fwd_kernel<<<blocks_for((int64_t)batch * w.rows), 256, 0, s>>>(
-      (const float *)ws, p.slices, batch, w.rows, bias, bias_len, act, pre, post);
+  if (e != hipSuccess) return e;
+  sk_reduce_kernel<true><<<blocks_for((int64_t)batch * w.rows), 256, 0, s>>>(a, bias, bias_len, act,
+                                                                             pre, post);
   return hipGetLastError();
 }
 
@@ -679,10 +1258,7 @@ size_t backward_workspace_bytes(const DevStore &w, int batch) {
     const int nseg = (w.rows + kDxSegRows - 1) / kDxSegRows;
     return (size_t)nseg * batch * w.cols * sizeof(float);
   }
-  if (route == 2) {
-    const GemmPlan p = plan_gemm(batch, w.rows, w.cols);
-    return p.slices > 1 ? (size_t)p.slices * batch * w.cols * sizeof(float) : 0;
-  }
+  if (route == 2) return plan_sk(batch, w.rows, w.cols).ws_bytes;
   return 0;
 }
 
@@ -694,7 +1270,7 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int route = dx_route(w, batch);
-  const int f = fmt_of(w.dtype);
+  const int f = kernel_fmt(w.dtype);
   if (ws_bytes < backward_workspace_bytes(w, batch)) return hipErrorInvalidValue;
   if (route == 3) {
 #define WH_DXG(D)                                                                         \
@@ -718,20 +1294,18 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     reduce_plain_kernel<<<blocks_for((int64_t)batch * w.cols), 256, 0, s>>>(
         (const float *)ws, nseg, (int64_t)batch * w.cols, dX);
   } else {
-    const GemmPlan p = plan_gemm(batch, w.rows, w.cols);
+    const SkPlan p = plan_sk(batch, w.rows, w.cols);
     GemmArgs a{w.body, w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
-               p.stages_per_slice, p.nstages, (float *)ws, p.slices == 1, nullptr, 0, -1, dX, nullptr};
-    dim3 grid(p.gx, p.gy, p.slices);
-#define WH_DXM(F)                                   \
-  gemm_kernel<F, true><<<grid, 256, 0, s>>>(a);     \
+               p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
+#define WH_DXM(F)                                           \
+  gemm_sk_kernel<F, true><<<p.blocks, 256, 0, s>>>(a);     \
   break;
     WH_FMT_SWITCH(f, WH_DXM)
 #undef WH_DXM
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (p.slices > 1)
-      reduce_plain_kernel<<<blocks_for((int64_t)batch * w.cols), 256, 0, s>>>(
-          (const float *)ws, p.slices, (int64_t)batch * w.cols, dX);
+    sk_reduce_kernel<false><<<blocks_for((int64_t)batch * w.cols), 256, 0, s>>>(a, nullptr, 0, -1,
+                                                                               dX, nullptr);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -26,6 +26,7 @@ struct DevStore {
   float minv;
   const uint8_t *body;
   const float *lut;  // 2^bits decoded values for formats of <= 8 bits
+  float tab16[16];   // host copy of the first 16 table values
 };
 
 // ---- codec.hip
@@ -60,5 +61,20 @@ size_t mse_workspace_bytes(int64_t n);
 // Kernel-selection knobs, exposed for sweeps: forward path for a batch
 // (0 = auto, 1 = GEMV, 2 = MFMA GEMM, 3 = generic element-wise).
 void set_forward_path(int path);
+
+// Tuning knobs: 0 batch-1 GEMV variant (0 row-group kernel, 1 all-loads-in-
+// flight kernel, 2 column-stationary kernel), 1 column-stationary rows per
+// block (0 = default), 2 column-stationary f64 in-lane accumulation, 3 chunks
+// per lane of the all-loads kernel (0 auto, 1: 2, 2: 4, 3: 1, 4: 8).  Returns
+// the previous value (-1 for an unknown key).
+// 4 register-B forward GEMM for <= 16-bit formats (1 on), 5 its workgroups
+// per CU (0 = 2).
+// 6 hardware FP8 converts / integer Int8 decode instead of tables (1 on),
+// 7 pair table for 4-bit formats (1 on).
+enum TuneKey {
+  kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
+  kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kNumTune = 8
+};
+int set_tuning(int key, int value);
 
 }  // namespace wh

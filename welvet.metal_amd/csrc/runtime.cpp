@@ -98,7 +98,13 @@ struct Store {
   double *bias = nullptr;
   int bias_len = 0;
 
-  DevStore dev() const { return DevStore{dtype, rows, cols, scale, minv, body, lut}; }
+  float tab16[16] = {};  // host copy of the first 16 decoded table values
+
+  DevStore dev() const {
+    DevStore d{dtype, rows, cols, scale, minv, body, lut, {}};
+    for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
+    return d;
+  }
   int64_t n() const { return (int64_t)rows * cols; }
 };
 
@@ -149,6 +155,8 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
   if (dtype_lut(dtype)) {
     WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
     WH_HIP(launch_lut(dtype, w->scale, w->minv, w->lut, s));
+    WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
+    WH_HIP(hipStreamSynchronize(s));
   }
   return ok();
 }
@@ -264,7 +272,8 @@ welvet_status session_alloc_io(welvet_dense_session *s) {
 
 welvet_status ensure_ws(welvet_dense_session *s, size_t bytes) {
   if (bytes <= s->ws_bytes) return ok();
-  WH_HIP(hipStreamSynchronize(s->stream));
+  // the old workspace may be in use on a caller's stream: drain the device
+  WH_HIP(hipDeviceSynchronize());
   if (s->ws) WH_HIP(hipFree(s->ws));
   s->ws = nullptr;
   WH_HIP(hipMalloc(&s->ws, bytes));
@@ -274,6 +283,9 @@ welvet_status ensure_ws(welvet_dense_session *s, size_t bytes) {
 
 welvet_status forward_device(welvet_dense_session *s, const float *x, float *pre, float *post,
                              hipStream_t st) {
+  // the kernel plan (and so the workspace) can change with the tuning knobs
+  welvet_status ws = ensure_ws(s, forward_workspace_bytes(s->W.dev(), s->batch));
+  if (ws.code) return ws;
   WH_HIP(launch_forward(s->W.dev(), s->batch, x, s->W.bias, s->W.bias_len, s->act, pre, post, s->ws,
                         s->ws_bytes, st));
   return ok();
@@ -487,7 +499,7 @@ welvet_status welvet_hip_dense_forward_device(welvet_dense_session *s, const flo
   if (((uintptr_t)d_x | (uintptr_t)d_pre | (uintptr_t)d_post) & 15)
     return make_status(kInvalid, "device pointers must be 16-byte aligned");
   std::lock_guard<std::mutex> lock(s->mu);
-  return forward_device(s, d_x, d_pre, d_post, stream ? (hipStream_t)stream : s->stream);
+  return forward_device(s, d_x, d_pre, d_post, (hipStream_t)stream);
 }
 
 welvet_status welvet_hip_dense_native(welvet_dense_session *s, uint8_t *out, size_t cap,
@@ -580,5 +592,7 @@ welvet_status welvet_hip_mse_f32(const float *pred, const float *target, size_t 
 }
 
 void welvet_hip_set_forward_path(int32_t path) { set_forward_path(path); }
+
+int32_t welvet_hip_set_tuning(int32_t key, int32_t value) { return set_tuning(key, value); }
 
 }  // extern "C"

@@ -95,6 +95,8 @@ def lib() -> C.CDLL:
         L.welvet_hip_mse_f32.restype = Status
         L.welvet_hip_set_forward_path.argtypes = [_i32]
         L.welvet_hip_set_forward_path.restype = None
+        L.welvet_hip_set_tuning.argtypes = [_i32, _i32]
+        L.welvet_hip_set_tuning.restype = _i32
         _LIB = L
     return _LIB
 
@@ -126,6 +128,14 @@ def init() -> None:
 
 def set_forward_path(path: int) -> None:
     lib().welvet_hip_set_forward_path(path)
+
+
+TUNE = {"gemv1": 0, "rows_per_block": 1, "acc64": 2, "cr": 3, "reg_gemm": 4, "gemm_occ": 5,
+        "fast_decode": 6, "pair_lut": 7}
+
+
+def set_tuning(key: str, value: int) -> int:
+    return lib().welvet_hip_set_tuning(TUNE[key], int(value))
 
 
 def forward(W, x, act=-1, dtype=1, bias=None, status=False):
