@@ -1,23 +1,27 @@
 """Headline benchmark: Dense forward over packed native weights, 4096 -> 11008.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fp8b1,...]
 
-A step is one Dense forward launch (welvet_hip_dense_forward_device) over one
-batch of synthetic input already resident in HBM.  The primary line is FP8
-E4M3, batch 1: value = packed-weight bytes per step / step time (GB/s), the
-BASELINE metric.  The same run measures NF4 batch 1 and FP8 / NF4 batch 64
-(TFLOP/s) and reports them under "results".
+A step is one Dense forward (welvet_hip_dense_forward_device) over one batch
+of synthetic input already resident in HBM.  The primary line is FP8 E4M3,
+batch 1: value = packed-weight bytes per step / step time (GB/s), the BASELINE
+metric; a batch-1 step is exactly one GEMV kernel launch.  The same run
+measures NF4 batch 1 and FP8 / NF4 batch 64 (TFLOP/s = 2*B*K*N / step time)
+and reports them under "results".
 
 Weights are N(0, 0.02) (generated on the device, seeded), x ~ N(0, 1).  Steps
 rotate over enough distinct weight copies that the working set exceeds
 512 MB, so the 256 MB MALL cannot serve repeated launches.  Timing: HIP events
-on the stream the kernels are launched on (torch's current stream), K steps
-between them after W warm-up steps; per-launch durations come from the same
-events (one pair per launch) in a second pass.
+on the stream the kernels are launched on (an explicit torch stream handed to
+the library), K back-to-back steps between them after W warm-up steps.
+
+roofline.traffic comes from the committed rocprofv3 --pmc passes
+(profiles/hbm_traffic.json); it is not measured live.
 
 cpu_baseline: the oracle's scalar port of the reference host path (per-element
 decode switch + f64 dot, oracle/oracle.c or_dense_forward_native), one thread,
-on the same workload for a bounded number of steps.
+on the same workload for a bounded number of full steps; an all-core OpenMP
+run of the same port is reported beside it.
 """
 from __future__ import annotations
 
@@ -84,25 +88,12 @@ def run_case(torch, pywelvet, dtype: int, batch: int, steps: int, warmup: int, s
     t1.record(stream)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
-    # per-launch durations from one event pair per launch
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(min(steps, 200))]
-    for i, (a, b) in enumerate(evs):
-        a.record(stream)
-        step(i)
-        b.record(stream)
-    torch.cuda.synchronize()
-    per = sorted(a.elapsed_time(b) for a, b in evs)
-    launch_ms = sum(per) / len(per)
     flops = 2.0 * batch * IN * OUT
     r = {
         "case": f"{pywelvet.DTYPE_NAMES[dtype]}_4096x11008_b{batch}",
         "weight_dtype": pywelvet.DTYPE_NAMES[dtype], "batch": batch, "in": IN, "out": OUT,
         "packed_bytes": wbytes, "weight_copies": copies, "ms_per_step": ms,
-        "launch_ms_mean": launch_ms, "launch_ms_median": per[len(per) // 2],
         "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12,
-        "hbm_gbs_per_launch": wbytes / (launch_ms * 1e-3) / 1e9,
-        "tflops_per_launch": flops / (launch_ms * 1e-3) / 1e12,
     }
     for s in sessions:
         s.close()
@@ -110,7 +101,8 @@ def run_case(torch, pywelvet, dtype: int, batch: int, steps: int, warmup: int, s
 
 
 def cpu_baseline(dtype: int, batch: int, seconds: float = 12.0):
-    """Oracle scalar port, one thread, on full 4096x11008 steps, bounded time."""
+    """Oracle scalar port on full 4096x11008 steps, bounded time: one thread
+    (the baseline), then every host core the run may use (reported beside)."""
     import numpy as np
     from oracle import Oracle
 
@@ -119,17 +111,41 @@ def cpu_baseline(dtype: int, batch: int, seconds: float = 12.0):
     W = rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02)
     x = rng.standard_normal((batch, IN), dtype=np.float32)
     raw, scale = O.pack(dtype, W)
-    steps, t = 0, 0.0
-    while t < seconds and steps < 50:
-        t0 = time.perf_counter()
-        O.forward_native(dtype, raw, scale, x, OUT, IN, -1, threads=1)
-        t += time.perf_counter() - t0
-        steps += 1
-    per = t / steps
+
+    def timed(threads, budget):
+        steps, t = 0, 0.0
+        while t < budget and steps < 200:
+            t0 = time.perf_counter()
+            O.forward_native(dtype, raw, scale, x, OUT, IN, -1, threads=threads)
+            t += time.perf_counter() - t0
+            steps += 1
+        return steps, t, t / steps
+
+    steps, t, per = timed(1, seconds)
+    ncores = min(16, len(os.sched_getaffinity(0)))  # the GPU box grants 16 host threads
+    msteps, mt, mper = timed(ncores, seconds / 3)
     return {"value": packed_bytes(dtype) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{steps} full steps of {pywelvet_name(dtype)} 4096x11008 b{batch} "
                       f"({t:.1f} s): per-element decode switch + f64 dot, 1 thread",
-            "ms_per_step": per * 1e3}
+            "ms_per_step": per * 1e3,
+            "all_cores": {"value": packed_bytes(dtype) / mper / 1e9, "unit": "GB/s",
+                          "cores": ncores, "ms_per_step": mper * 1e3,
+                          "sample": f"{msteps} full steps ({mt:.1f} s), OpenMP over rows"}}
+
+
+def calibrate_copy(torch, mib: int = 256, launches: int = 5):
+    """Element-wise copy out = in * 1 of `mib` MiB, `launches` times: each launch
+    reads and writes exactly mib MiB, the yardstick for FETCH_SIZE/WRITE_SIZE."""
+    dev = torch.device("cuda:0")
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy": {"bytes_read": n * 4, "bytes_written": n * 4,
+                                         "launches": launches}}), flush=True)
 
 
 def pywelvet_name(dtype):
@@ -144,12 +160,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of cases: fp8b1,nf4b1,fp8b64,nf4b64")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain copy kernel of known size (for scaling HBM counters)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
               file=sys.stderr)
         sys.exit(2)
     import torch
+    if a.calibrate_copy:
+        calibrate_copy(torch)
+        return
     import pywelvet
 
     pywelvet.init()
@@ -163,14 +184,19 @@ def main():
         print(f"# {name}: {results[name]['hbm_gbs']:.1f} GB/s  {results[name]['tflops']:.2f} TFLOP/s"
               f"  {results[name]['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
     prim = results.get("fp8b1") or next(iter(results.values()))
+    # One step of a batch-1 case is exactly one GEMV launch, so the timed
+    # region's mean step time is that kernel's mean launch duration.
     if prim["batch"] == 1:
-        ach = prim["packed_bytes"] / (prim["launch_ms_mean"] * 1e-3) / 1e9
+        ach = prim["hbm_gbs"]
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": ach / HBM_PEAK, "traffic": None}
+                "frac": ach / HBM_PEAK, "traffic": measured_traffic(prim_name(results, prim))}
     else:
-        ach = prim["tflops_per_launch"]
+        ach = prim["tflops"]
         roof = {"bound": "mfma", "achieved": ach, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-                "frac": ach / FP32_MFMA_PEAK, "traffic": None}
+                "frac": ach / FP32_MFMA_PEAK, "traffic": measured_traffic(prim_name(results, prim))}
+    for r in results.values():
+        r["roofline_frac"] = (r["hbm_gbs"] / HBM_PEAK if r["batch"] == 1
+                              else r["tflops"] / FP32_MFMA_PEAK)
     line = {
         "metric": METRIC, "value": prim["hbm_gbs"] if prim["batch"] == 1 else prim["tflops"],
         "unit": "GB/s" if prim["batch"] == 1 else "TFLOP/s", "n_gpus": 1, "steps": a.steps,
@@ -181,12 +207,30 @@ def main():
                    "batch": prim["batch"], "weight_dtype": prim["weight_dtype"],
                    "weight_copies": prim["weight_copies"], "act": "linear"},
         "roofline": roof,
-        "results": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+        "results": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},
     }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(prim["weight_dtype"] == "nf4" and 26 or 4, prim["batch"])
     print(json.dumps(line), flush=True)
+
+
+def prim_name(results, prim):
+    return next(k for k, v in results.items() if v is prim)
+
+
+def measured_traffic(case: str):
+    """HBM bytes per launch of the case's kernel from the committed rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE passes, each scaled by what the counter reads
+    for a copy kernel of known size (profiles/hbm_traffic.json); None when that
+    case was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)["cases"][case]
+    except (OSError, KeyError, ValueError):
+        return None
+    return rec["bytes_per_launch"]
 
 
 if __name__ == "__main__":

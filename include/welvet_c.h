@@ -105,8 +105,18 @@ WELVET_API welvet_status welvet_hip_mse_f32(const float *pred, const float *targ
 /* Kernel route of the forward: 0 auto, 1 GEMV, 2 MFMA GEMM, 3 element-wise. */
 WELVET_API void welvet_hip_set_forward_path(int32_t path);
 /* Kernel tuning knob `key` := value, returns the previous value (-1 = unknown
- * key).  Keys: 0 batch-1 column-stationary GEMV (1 on), 1 its rows per block
- * (0 = default), 2 its in-lane f64 accumulation (1 on). */
+ * key).  Process-wide; results stay within the same tolerance whatever the
+ * setting.  Keys (default in brackets):
+ *   0 batch-1 GEMV kernel: 0 row-group, 1 all-loads-in-flight [1],
+ *     2 column-stationary
+ *   1 column-stationary rows per block [0 = 16]
+ *   2 column-stationary in-lane f64 accumulation [0]
+ *   3 all-loads-in-flight chunks per lane: 0 auto, 1 two, 2 four, 3 one,
+ *     4 eight [0]
+ *   4 register-B MFMA GEMM for formats of <= 16 bits [1]
+ *   5 its workgroups per CU [0 = 2]
+ *   6 hardware FP8 conversions and integer Int8 decode instead of tables [1]
+ *   7 byte-pair decode table for 4-bit formats [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

@@ -141,6 +141,29 @@ def test_session_reuse(oracle):
             assert_close(post, rpost, 512, f"iter {i}")
 
 
+@pytest.mark.parametrize("dtype", [4, 26, 1])
+def test_gemm_session_repeat(oracle, dtype):
+    """Repeated MFMA launches on one session: the stream-K tile counters the
+    GEMMs leave behind must let every later forward and dX come out right."""
+    rng = np.random.default_rng(17 + dtype)
+    out, inn, batch = 1500, 2048, 48
+    W = rng.normal(0, 0.05, (out, inn)).astype(np.float32)
+    Wd = oracle_weights(oracle, dtype, W)
+    bias = rng.normal(0, 1, out)
+    with pywelvet.Session(W, batch=batch, act=1, dtype=dtype, bias=bias) as s:
+        for i in range(4):
+            x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+            pre, post = s.execute(x)
+            rpre, rpost = oracle.forward(Wd, x, 1, bias)
+            assert_close(pre, rpre, inn, f"pre iter {i}")
+            assert_close(post, rpost, inn, f"post iter {i}")
+            gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+            dX, dW = s.backward(x, pre, gy)
+            _, rdX, rdW = oracle.backward(Wd, x, pre, gy, 1)
+            assert_close(dX, rdX, out, f"dX iter {i}")
+            assert_bit_equal(dW, rdW, f"dW iter {i}")
+
+
 @pytest.mark.parametrize("dtype", [1, 0, 4, 9, 26, 14, 12, 27, 20])
 @pytest.mark.parametrize("batch", [1, 2, 5, 40])
 def test_backward(oracle, dtype, batch):

@@ -1,0 +1,370 @@
+"""Pins for the oracle functions the reference's golden vectors do not reach:
+the Dense forward/backward contract, activations, fixed-scale re-encode,
+SGD and MSE.  Each expectation is computed a different way than the oracle
+computes it: exact rational arithmetic with an explicit round-to-nearest-even
+to f32, integer arithmetic on dyadic inputs (where every summation order is
+exact), textbook formulas, finite differences and structural invariants.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import ACT, DTYPE_NAMES
+
+
+def rnd32(q: Fraction) -> np.float32:
+    """Round an exact rational to the nearest f32, ties to even (normal range)."""
+    if q == 0:
+        return np.float32(0.0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    assert -126 <= e <= 127, "outside the f32 normal range"
+    ulp = Fraction(2) ** (e - 23)
+    n = a / ulp
+    fl = n.numerator // n.denominator
+    rem = n - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return np.float32(sign * float(fl * ulp))
+
+
+def F(v) -> Fraction:
+    return Fraction(float(v))
+
+
+def test_rnd32_helper():
+    assert rnd32(Fraction(1) + Fraction(1, 2**24)) == np.float32(1.0)  # tie -> even
+    assert rnd32(Fraction(1) + Fraction(3, 2**24)) == np.float32(1.0 + 2**-22)
+    for v in np.random.default_rng(0).normal(0, 100, 200).astype(np.float32):
+        assert rnd32(F(v)) == v
+
+
+# ---------------------------------------------------------------- forward
+def test_forward_dyadic_brute_force(oracle):
+    """Dyadic W, x, bias: every partial sum is exact, so pre must equal the
+    integer product exactly; a transposed operand, a dropped bias or a wrong
+    index changes the result."""
+    rng = np.random.default_rng(1)
+    for out, inn, batch in ((3, 5, 2), (7, 16, 3), (1, 1, 1), (12, 33, 4)):
+        Wi = rng.integers(-16, 17, (out, inn))
+        xi = rng.integers(-16, 17, (batch, inn))
+        bi = rng.integers(-64, 65, out)
+        W = Wi / 8.0
+        x = (xi / 4.0).astype(np.float32)
+        bias = bi / 32.0
+        blen = max(1, out - 1)  # the last output gets no bias
+        exact = (xi @ Wi.T).astype(np.int64)  # in units of 1/32
+        for act in (-1, 0, 5, 6):
+            pre, post = oracle.forward(W, x, act, bias[:blen])
+            want = exact.astype(np.float64) / 32.0
+            want[:, :blen] += bias[:blen]
+            np.testing.assert_array_equal(pre, want.astype(np.float32))
+            v = pre.astype(np.float64)
+            ref = {-1: v, 0: np.where(v > 0, v, 0.0), 5: np.where(v < 0, v * 0.01, v),
+                   6: np.where(v < 0, 0.0, v * v)}[act]
+            np.testing.assert_array_equal(post, ref.astype(np.float32))
+
+
+def test_forward_rounds_an_f64_sum_once(oracle):
+    """pre = fl32(sum w*x) with the sum carried far beyond f32 precision: equal
+    to the correctly rounded exact sum (within one f32 ulp on near-ties), and
+    different from an f32 running sum on these inputs."""
+    rng = np.random.default_rng(2)
+    W = rng.normal(0, 1, (40, 24))
+    x = rng.normal(0, 1, (2, 24)).astype(np.float32)
+    pre, _ = oracle.forward(W, x, -1)
+    f32_differs = 0
+    for b in range(2):
+        for o in range(40):
+            exact = sum(F(W[o, k]) * F(x[b, k]) for k in range(24))
+            want = rnd32(exact)
+            assert abs(float(pre[b, o]) - float(want)) <= abs(np.spacing(np.float32(want))), (b, o)
+            acc = np.float32(0)
+            for k in range(24):
+                acc = np.float32(acc + np.float32(np.float32(W[o, k]) * x[b, k]))
+            f32_differs += acc != want
+    assert f32_differs > 0
+
+
+# --------------------------------------------------------------- backward
+def test_backward_dyadic_brute_force(oracle):
+    rng = np.random.default_rng(3)
+    out, inn, batch = 6, 9, 4
+    Wi = rng.integers(-16, 17, (out, inn))
+    xi = rng.integers(-16, 17, (batch, inn))
+    gi = rng.integers(-16, 17, (batch, out))
+    pi = rng.integers(-4, 5, (batch, out))
+    W, x, gy, pre = Wi / 8.0, (xi / 4.0).astype(np.float32), (gi / 4.0).astype(np.float32), \
+        (pi / 2.0).astype(np.float32)
+    for act, mask in ((-1, np.ones_like(pi)), (0, (pi > 0).astype(np.int64))):
+        dpre, dX, dW = oracle.backward(W, x, pre, gy, act)
+        dpi = gi * mask  # units of 1/4
+        np.testing.assert_array_equal(dpre, (dpi / 4.0).astype(np.float32))
+        np.testing.assert_array_equal(dX, ((dpi @ Wi) / 32.0).astype(np.float32))  # not Wi.T
+        np.testing.assert_array_equal(dW, ((dpi.T @ xi) / 16.0).astype(np.float32))
+
+
+def test_backward_dw_is_a_sequential_fused_multiply_add(oracle):
+    """dW[o,i] = fl32(acc + g*x) over the batch with the product exact: the
+    exact-rational model of that recurrence, which differs from a rounded
+    product followed by a rounded add on some of these entries."""
+    rng = np.random.default_rng(4)
+    out, inn, batch = 5, 7, 6
+    W = np.zeros((out, inn))
+    x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+    gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    pre = np.ones((batch, out), np.float32)
+    _, _, dW = oracle.backward(W, x, pre, gy, -1)
+    unfused_differs = 0
+    for o in range(out):
+        for i in range(inn):
+            acc = np.float32(0)
+            acc_u = np.float32(0)
+            for b in range(batch):
+                acc = rnd32(F(acc) + F(gy[b, o]) * F(x[b, i]))
+                acc_u = np.float32(acc_u + np.float32(gy[b, o] * x[b, i]))
+            assert dW[o, i] == acc, (o, i)
+            unfused_differs += acc_u != acc
+    assert unfused_differs > 0
+
+
+# ------------------------------------------------------------ activations
+def _gelu_tanh(x):  # Hendrycks & Gimpel's tanh approximation
+    return 0.5 * x * (1 + math.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+TEXTBOOK = {
+    "silu": lambda x: x / (1 + math.exp(-x)),
+    "gelu": _gelu_tanh,
+    "tanh": math.tanh,
+    "sigmoid": lambda x: 1 / (1 + math.exp(-x)),
+}
+
+
+@pytest.mark.parametrize("name", list(TEXTBOOK))
+def test_smooth_activations_match_textbook(oracle, name):
+    act = ACT[name]
+    f = TEXTBOOK[name]
+    for v in np.linspace(-12, 12, 481).astype(np.float32):
+        got = oracle.act(float(v), act)
+        want = f(float(v))
+        # 1 + tanh(u) cancels for GELU at large negative x: absolute slack there
+        assert abs(got - want) <= 2 * abs(np.spacing(np.float32(want))) + 1e-14, (name, v)
+
+
+@pytest.mark.parametrize("name", list(TEXTBOOK) + ["relu", "leakyrelu", "relu2", "linear"])
+def test_derivatives_match_finite_differences(oracle, name):
+    act = ACT[name]
+    exact = {"relu": lambda x: max(x, 0.0), "leakyrelu": lambda x: x if x >= 0 else 0.01 * x,
+             "relu2": lambda x: 0.0 if x < 0 else x * x, "linear": lambda x: x}
+    f = TEXTBOOK.get(name) or exact[name]
+    h = 1e-5
+    for v in np.linspace(-6, 6, 97).astype(np.float32):
+        x = float(v)
+        if abs(x) < 2 * h:
+            continue  # the kinks at 0
+        fd = (f(x + h) - f(x - h)) / (2 * h)
+        got = oracle.act_prime(x, act)
+        assert abs(got - fd) <= 2e-4 * max(1.0, abs(fd)), (name, x, got, fd)
+
+
+def test_activation_special_points(oracle):
+    assert oracle.act(0.0, ACT["sigmoid"]) == 0.5
+    for name in ("silu", "gelu", "tanh", "relu", "relu2", "leakyrelu"):
+        assert oracle.act(0.0, ACT[name]) == 0.0
+    assert oracle.act(18.5, ACT["tanh"]) == 1.0 and oracle.act(-18.5, ACT["tanh"]) == -1.0
+    assert oracle.act(30.0, ACT["gelu"]) == 30.0
+    assert oracle.act_prime(0.0, ACT["relu"]) == 0.0      # v > 0 ? 1 : 0
+    assert oracle.act_prime(0.0, ACT["relu2"]) == 0.0
+    assert oracle.act_prime(-1.0, ACT["leakyrelu"]) == np.float32(0.01)
+    assert oracle.act_prime(0.0, ACT["tanh"]) == 1.0
+    assert oracle.act_prime(0.0, ACT["sigmoid"]) == 0.25
+    for unknown in (7, 42, -2):  # unknown ids act as Linear
+        assert oracle.act(-3.5, unknown) == -3.5 and oracle.act_prime(-3.5, unknown) == 1.0
+
+
+# ---------------------------------------------------- fixed-scale re-encode
+NATIVE = [d for d in range(34) if d not in (0, 1)]
+
+
+# Codes that decode to a value which re-encodes to another code of the same
+# value: E4M3 -0 and subnormals (all decode to zero, re-encode to 0x00) and the
+# 64-bit unsigned formats (the f32 value cannot hold a 64-bit code).
+LOSSY_CODES = ("uint64", "uint", "uintptr")
+
+
+def _byte_fixed_point_expected(dtype, raw, dec, i):
+    name = DTYPE_NAMES[dtype]
+    if name in LOSSY_CODES:
+        return False
+    if name == "fp8e4m3" and dec[i] == 0 and raw[i] != 0:
+        return False
+    return True
+
+
+@pytest.mark.parametrize("dtype", NATIVE, ids=[DTYPE_NAMES[d] for d in NATIVE])
+def test_set_decoded_value_is_a_fixed_point(oracle, dtype):
+    """Re-encoding an element's own decoded value keeps that value
+    (decode(encode(decode(c))) == decode(c)) and, for every code that is the
+    only one of its value, keeps every byte."""
+    rng = np.random.default_rng(dtype)
+    n = 37
+    for w in (rng.normal(0, 0.05, n), rng.uniform(-3, 3, n)):
+        raw, scale = oracle.pack(dtype, w.astype(np.float32))
+        dec = oracle.decode(dtype, raw, scale, n)
+        for i in range(n):
+            r2 = raw.copy()
+            assert oracle.set(dtype, r2, scale, i, n, float(dec[i])) == 0
+            assert oracle.decode(dtype, r2, scale, n)[i] == dec[i], (DTYPE_NAMES[dtype], i)
+            if _byte_fixed_point_expected(dtype, raw, dec, i):
+                np.testing.assert_array_equal(r2, raw, err_msg=f"{DTYPE_NAMES[dtype]} i={i}")
+
+
+@pytest.mark.parametrize("dtype", NATIVE, ids=[DTYPE_NAMES[d] for d in NATIVE])
+def test_set_touches_only_its_element(oracle, dtype):
+    rng = np.random.default_rng(100 + dtype)
+    n = 29
+    raw, scale = oracle.pack(dtype, rng.uniform(-2, 2, n).astype(np.float32))
+    before = oracle.decode(dtype, raw, scale, n)
+    for i in (0, 1, 7, 13, n - 1):
+        r2 = raw.copy()
+        oracle.set(dtype, r2, scale, i, n, float(rng.uniform(-2, 2)))
+        after = oracle.decode(dtype, r2, scale, n)
+        others = np.arange(n) != i
+        np.testing.assert_array_equal(after[others], before[others],
+                                      err_msg=f"{DTYPE_NAMES[dtype]} i={i}")
+
+
+def test_set_signed_integer_quantizer(oracle):
+    """Int8/Int4/Int16 with a power-of-two scale: code = clamp(round-half-away(v/s))."""
+    for dtype, lo, hi in ((9, -128, 127), (14, -8, 7), (8, -32768, 32767)):
+        n = 8
+        raw, scale = oracle.pack(dtype, np.full(n, 0.0, np.float32))
+        s = float(np.float32(scale))
+        for v in (0.3, -0.3, 2.5, -2.5, 1e9, -1e9, 7.49, 126.5):
+            r = raw.copy()
+            oracle.set(dtype, r, scale, 3, n, v * s)
+            q = math.floor(abs(v) + 0.5) * (1 if v >= 0 else -1)
+            want = min(max(q, lo), hi) * s
+            assert oracle.decode(dtype, r, scale, n)[3] == np.float32(want), (dtype, v)
+
+
+def test_set_saturating_clamp_bounds(oracle):
+    """The float clamp bounds 2147483647.0f and 4294967295.0f are 2^31 and 2^32:
+    the following conversion saturates (arm64)."""
+    raw, scale = oracle.pack(7, np.array([1.0, -1.0], np.float32))  # Int32, scale 1/(2^31-1)
+    oracle.set(7, raw, scale, 0, 2, 10.0)
+    assert raw[:4].view("<i4")[0] == 2**31 - 1
+    oracle.set(7, raw, scale, 0, 2, -10.0)
+    assert raw[:4].view("<i4")[0] == -2**31
+
+
+# ------------------------------------------------------------------- SGD
+def test_native_sgd_zero_rate_is_identity(oracle):
+    """lr = 0 re-encodes every element's own value: values are unchanged, and
+    bytes too wherever the code is the only one of its value."""
+    rng = np.random.default_rng(7)
+    n = 50
+    for dtype in NATIVE:
+        raw, scale = oracle.pack(dtype, rng.normal(0, 0.3, n).astype(np.float32))
+        dec = oracle.decode(dtype, raw, scale, n)
+        r2 = raw.copy()
+        assert oracle.native_sgd(dtype, r2, scale, n, rng.normal(0, 1, n), 0.0) == 0
+        np.testing.assert_array_equal(oracle.decode(dtype, r2, scale, n), dec)
+        if DTYPE_NAMES[dtype] not in LOSSY_CODES + ("fp8e4m3",):
+            np.testing.assert_array_equal(r2, raw, err_msg=DTYPE_NAMES[dtype])
+
+
+def test_native_sgd_exact_grid_steps(oracle):
+    """Int8 with scale 2^-6 (absmax 127/64) and steps that land on the grid:
+    the new codes are exactly old - lr*g / scale."""
+    n = 16
+    rng = np.random.default_rng(8)
+    codes = rng.integers(-100, 100, n)
+    codes[0] = 127
+    w = (codes / 64.0).astype(np.float32)
+    raw, scale = oracle.pack(9, w)
+    assert np.float32(scale) == np.float32(2**-6)
+    steps = rng.integers(-20, 21, n)
+    steps[0] = 0
+    g = (steps / 64.0 / 0.5).astype(np.float32)  # lr 0.5
+    assert oracle.native_sgd(9, raw, scale, n, g, 0.5) == 0
+    np.testing.assert_array_equal(raw.view(np.int8).astype(np.int64),
+                                  np.clip(codes - steps, -128, 127))
+
+
+def test_native_sgd_is_rounded_difference_then_reencode(oracle):
+    """E4M3: each new code is the encoder applied to fl32(old - lr*g), with the
+    encoder pinned by the reference's own tables."""
+    rng = np.random.default_rng(9)
+    n = 64
+    raw, scale = oracle.pack(4, rng.normal(0, 1, n).astype(np.float32))
+    old = oracle.decode(4, raw, scale, n)
+    g = rng.normal(0, 1, n).astype(np.float32)
+    lr = 0.37
+    r2 = raw.copy()
+    oracle.native_sgd(4, r2, scale, n, g, lr)
+    want = [int(oracle.encode_many(2, np.array([rnd32(F(old[i]) - Fraction(lr) * F(g[i]))],
+                                              np.float32))[0]) for i in range(n)]
+    assert list(r2) == want
+
+
+def test_sgd_f32_rounds_the_step_first(oracle):
+    rng = np.random.default_rng(10)
+    w = rng.normal(0, 1, 300).astype(np.float32)
+    g = rng.normal(0, 1, 300).astype(np.float32)
+    lr = 0.1
+    got = w.copy()
+    oracle.sgd_f32(got, g, lr)
+    one_rounding_differs = 0
+    for i in range(300):
+        step = rnd32(Fraction(lr) * F(g[i]))
+        assert got[i] == rnd32(F(w[i]) - F(step)), i
+        one_rounding_differs += rnd32(F(w[i]) - Fraction(lr) * F(g[i])) != got[i]
+    assert one_rounding_differs > 0
+
+
+def test_float64_native_sgd_closed_form(oracle):
+    rng = np.random.default_rng(11)
+    w = rng.normal(0, 1, 20)
+    raw = np.frombuffer(w.tobytes(), np.uint8).copy()
+    g = rng.normal(0, 1, 20).astype(np.float32)
+    assert oracle.native_sgd(0, raw, 1.0, 20, g, 0.25) == 0
+    np.testing.assert_array_equal(raw.view("<f8"), w - 0.25 * g.astype(np.float64))
+
+
+# ------------------------------------------------------------------- MSE
+def test_mse_exact_rationals(oracle):
+    rng = np.random.default_rng(12)
+    p = rng.normal(0, 1, 9).astype(np.float32)
+    t = rng.normal(0, 1, 9).astype(np.float32)
+    exact = sum((F(a) - F(b)) ** 2 for a, b in zip(p, t)) / 9
+    assert abs(oracle.mse(p, t) - float(exact)) <= 4 * abs(np.spacing(float(exact)))
+    g = oracle.mse_grad(p, t)
+    for i in range(9):
+        assert g[i] == rnd32(2 * (F(p[i]) - F(t[i])) / 9)
+    assert oracle.mse(p, p) == 0.0 and not np.any(oracle.mse_grad(p, p))
+
+
+# ------------------------------------------------------- CPU baseline path
+@pytest.mark.parametrize("dtype", [1, 0, 4, 9, 26, 16, 27, 33, 10])
+def test_forward_native_is_decode_then_forward(oracle, dtype):
+    """The timed CPU baseline (per-element decode inside the dot) gives the
+    same bits as decode_f64 followed by the forward contract, single- and
+    multi-threaded."""
+    rng = np.random.default_rng(dtype)
+    W = rng.normal(0, 0.2, (33, 70)).astype(np.float32)
+    x = rng.normal(0, 1, (3, 70)).astype(np.float32)
+    bias = rng.normal(0, 1, 20)
+    raw, scale = oracle.pack(dtype, W)
+    Wd = oracle.decode_f64(dtype, raw, scale, W.size).reshape(W.shape)
+    rpre, rpost = oracle.forward(Wd, x, 3, bias)
+    for threads in (1, 4):
+        pre, post = oracle.forward_native(dtype, raw, scale, x, 33, 70, 3, bias, threads=threads)
+        np.testing.assert_array_equal(pre, rpre)
+        np.testing.assert_array_equal(post, rpost)

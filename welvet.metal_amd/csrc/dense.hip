@@ -570,8 +570,11 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(DevStore w, int batch
 // one per workgroup (two resident per CU), so every CU gets the same work
 // whatever the tile count.  Each share stages A and decoded W tiles in
 // double-buffered LDS (the next stage's global loads are in flight during
-// the current stage's MFMAs), writes one partial tile per tile it touches,
-// and sk_reduce_kernel adds a tile's partials in workgroup order in f64.
+// the current stage's MFMAs) and writes one partial tile per tile it
+// touches; sk_reduce_kernel then adds each tile's partials in workgroup
+// order in f64.  (Folding that sum into the GEMM, with the last workgroup to
+// finish a tile doing it, needs an agent-scope release per partial: the L2
+// write-back it costs made the forward GEMM 2.5x slower.)
 struct GemmArgs {
   const uint8_t *body;
   const float *lut;
@@ -582,7 +585,7 @@ struct GemmArgs {
   int gx, gy, nst;    // tiles along N, along M; k stages
   int per_block, maxspan;
   float *ws;          // [blocks][maxspan][bm][bn] partial tiles
-  int bm, bn;         // tile shape of the kernel that wrote ws
+  int bm, bn;         // tile shape
 };
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -827,26 +830,49 @@ __global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs a) {
   }
 }
 
-// Sum of a tile's stream-K partials in workgroup order (f64); the forward
-// applies bias + activation, dX stores fl32 of the sum.
+// Sum of a tile's stream-K partials in workgroup order (f64).  Grid: x =
+// tile, y = 1024-element slice of the tile; each thread adds four adjacent
+// outputs with float4 loads.  The forward applies bias + activation, dX
+// stores fl32 of the sum.
 template <bool FWD>
 __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double *bias, int bias_len,
                                                         int act, float *out, float *post) {
-  const int64_t total = (int64_t)a.M * a.N;
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * 256) {
-    const int m = (int)(idx / a.N), n = (int)(idx % a.N);
-    const int ty = m / a.bm, tx = n / a.bn, t = ty * a.gx + tx;
-    const int b0 = (int)((int64_t)t * a.nst / a.per_block);
-    const int b1 = (int)(((int64_t)(t + 1) * a.nst - 1) / a.per_block);
-    const int off = (m - ty * a.bm) * a.bn + (n - tx * a.bn);
-    double s = 0;
-    for (int b = b0; b <= b1; ++b) {
-      const int slot = t - (int)((int64_t)b * a.per_block / a.nst);
-      s += (double)a.ws[((int64_t)b * a.maxspan + slot) * (a.bm * a.bn) + off];
+  const int t = blockIdx.x;
+  const int b0 = (int)((int64_t)t * a.nst / a.per_block);
+  const int b1 = (int)(((int64_t)(t + 1) * a.nst - 1) / a.per_block);
+  const int tile = a.bm * a.bn;
+  const int off = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (off >= tile) return;
+  const int m = (t / a.gx) * a.bm + off / a.bn, n = (t % a.gx) * a.bn + off % a.bn;
+  if (m >= a.M) return;
+  double sum[4] = {0, 0, 0, 0};
+  // all loads of a group of 8 partials are issued before the first add
+  for (int g = b0; g <= b1; g += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int b = g + i;
+      if (b <= b1) {
+        const int slot = t - (int)((int64_t)b * a.per_block / a.nst);
+        v[i] = *(const float4 *)(a.ws + ((int64_t)b * a.maxspan + slot) * tile + off);
+      }
     }
-    if constexpr (FWD) bias_act_store(s, n, bias, bias_len, act, out, post, idx);
-    else out[idx] = (float)s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (g + i <= b1) {
+        sum[0] += (double)v[i].x;
+        sum[1] += (double)v[i].y;
+        sum[2] += (double)v[i].z;
+        sum[3] += (double)v[i].w;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (n + i >= a.N) break;
+    const int64_t idx = (int64_t)m * a.N + n + i;
+    if constexpr (FWD) bias_act_store(sum[i], n + i, bias, bias_len, act, out, post, idx);
+    else out[idx] = (float)sum[i];
   }
 }
 
@@ -1078,6 +1104,10 @@ SkPlan plan_sk(int M, int K, int N, int bm = kBM, int bn = kBN, int occ = 2) {
   return p;
 }
 
+dim3 sk_reduce_grid(const SkPlan &p) {
+  return dim3(p.gx * p.gy, (p.bm * p.bn / 4 + 255) / 256);
+}
+
 bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // formats of <= 16 bits
 
 // Forward GEMM plan: the register-B kernel for <= 16-bit formats, else the
@@ -1239,8 +1269,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  sk_reduce_kernel<true><<<blocks_for((int64_t)batch * w.rows), 256, 0, s>>>(a, bias, bias_len, act,
-                                                                             pre, post);
+  sk_reduce_kernel<true><<<sk_reduce_grid(p), 256, 0, s>>>(a, bias, bias_len, act, pre, post);
   return hipGetLastError();
 }
 
@@ -1304,8 +1333,7 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
 #undef WH_DXM
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    sk_reduce_kernel<false><<<blocks_for((int64_t)batch * w.cols), 256, 0, s>>>(a, nullptr, 0, -1,
-                                                                               dX, nullptr);
+    sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
