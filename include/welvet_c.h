@@ -102,6 +102,60 @@ WELVET_API welvet_status welvet_hip_dense_sgd(welvet_dense_session *s, const flo
 /* MSE loss and/or gradient of n values (host pointers; either output may be NULL). */
 WELVET_API welvet_status welvet_hip_mse_f32(const float *pred, const float *target, size_t n,
                                             double *loss, float *grad);
+/* ---- volume runtime over Dense cells (extensions) ------------------------
+ * The reference runs volumes through its C++ API (architecture::Grid,
+ * runtime::forward/backward::volume_dense, runtime::training::step_dense);
+ * these entry points expose the same sequencing with its argument meaning
+ * and error messages.  Every cell's packed weights and activations stay in
+ * HBM; batch is fixed for the whole grid at creation. */
+typedef struct welvet_hip_grid welvet_hip_grid;
+/* architecture::new_grid grid.cpp:31-60 (a dimension < 1 becomes 1). */
+WELVET_API welvet_status welvet_hip_grid_new(int32_t depth, int32_t rows, int32_t cols,
+                                             int32_t layers_per_cell, int32_t batch,
+                                             welvet_hip_grid **g);
+WELVET_API void welvet_hip_grid_release(welvet_hip_grid *g);
+/* architecture::bind_dense grid.cpp:109-117 of dense::new_layer dense.cpp:101-119:
+ * W_init [out*in] row-major f32 encoded into dtype; bias as in mount. */
+WELVET_API welvet_status welvet_hip_grid_bind_dense(welvet_hip_grid *g, int32_t z, int32_t y,
+                                                    int32_t x, int32_t l, int32_t in, int32_t out,
+                                                    int32_t act, int32_t dtype, const float *W_init,
+                                                    const double *bias, size_t bias_len);
+/* architecture::set_remote_link grid.cpp:97-107: the cell reads the recorded
+ * post of (tz,ty,tx,tl) instead of the previous hop's output. */
+WELVET_API welvet_status welvet_hip_grid_set_remote_link(welvet_hip_grid *g, int32_t z, int32_t y,
+                                                         int32_t x, int32_t l, int32_t tz,
+                                                         int32_t ty, int32_t tx, int32_t tl);
+/* CellMeta::is_disabled: the hop skips the cell (forward.cpp:90). */
+WELVET_API welvet_status welvet_hip_grid_set_disabled(welvet_hip_grid *g, int32_t z, int32_t y,
+                                                      int32_t x, int32_t l, int32_t disabled);
+/* runtime::forward::volume_dense forward.cpp:74-132 in hop order z,y,x,l
+ * (grid.cpp:82-95): x [batch*in] -> y [batch*out], out = the last hop's width. */
+WELVET_API welvet_status welvet_hip_volume_forward(welvet_hip_grid *g, const float *x, int32_t in,
+                                                   float *y, int32_t out);
+/* The same on device pointers, enqueued on `stream` (NULL = null stream). */
+WELVET_API welvet_status welvet_hip_volume_forward_device(welvet_hip_grid *g, const float *d_x,
+                                                          int32_t in, float *d_y, int32_t out,
+                                                          void *stream);
+/* A volume forward followed by runtime::training::step_dense training.cpp:161-184:
+ * *loss = MSE(y, target) (target [batch*out]), backward through the tape in
+ * reverse (backward.cpp:88-127), SGD of every cell in forward order with
+ * re-encode (training.cpp:61-159).  y [batch*out] receives the forward
+ * output when non-NULL. */
+WELVET_API welvet_status welvet_hip_volume_train_step(welvet_hip_grid *g, const float *x,
+                                                      int32_t in, const float *target, int32_t out,
+                                                      double lr, double *loss, float *y);
+/* The same on device pointers on `stream`; returns after the step completed. */
+WELVET_API welvet_status welvet_hip_volume_train_step_device(welvet_hip_grid *g, const float *d_x,
+                                                             int32_t in, const float *d_target,
+                                                             int32_t out, double lr, double *loss,
+                                                             void *stream);
+/* WeightStore::export_f32 / native bytes of one bound cell. */
+WELVET_API welvet_status welvet_hip_grid_export_f32(welvet_hip_grid *g, int32_t z, int32_t y,
+                                                    int32_t x, int32_t l, float *W_out);
+WELVET_API welvet_status welvet_hip_grid_native(welvet_hip_grid *g, int32_t z, int32_t y,
+                                                int32_t x, int32_t l, uint8_t *out, size_t cap,
+                                                size_t *len, float *scale);
+
 /* Kernel route of the forward: 0 auto, 1 GEMV, 2 MFMA GEMM, 3 element-wise. */
 WELVET_API void welvet_hip_set_forward_path(int32_t path);
 /* Kernel tuning knob `key` := value, returns the previous value (-1 = unknown

@@ -268,3 +268,125 @@ class Reference:
 
 def have_reference() -> bool:
     return os.path.exists(REF_SO)
+
+
+class Volume:
+    """CPU restatement of the volume runtime over Dense cells.
+
+    TEST INFRASTRUCTURE ONLY.  Sequencing follows the reference:
+      hop order z, y, x, l                      src/architecture/grid.cpp:82-95
+      runtime::forward::volume_dense            src/runtime/forward.cpp:74-132
+        (disabled cells skipped, an enabled cell without an op, a remote hop
+        without a recorded post, or a width mismatch is an error)
+      runtime::backward::volume_dense           src/runtime/backward.cpp:88-127
+        (tape in reverse; each step's input gradient feeds the step before it)
+      runtime::training::sgd_dense, step_dense  src/runtime/training.cpp:61-184
+        (LR 0 is an error; SGD per cell in forward order, the first failing
+        cell stops the rest)
+    and every arithmetic step is one of this oracle's pinned Dense functions.
+    Results are (code, message, ...) like the C ABI's status.
+    """
+
+    def __init__(self, oracle: Oracle, depth: int, rows: int, cols: int, layers: int, batch: int):
+        self.O = oracle
+        self.dims = (max(1, depth), max(1, rows), max(1, cols), max(1, layers))
+        self.batch = batch
+        self.cells = {}
+        self.remote = {}
+        self.disabled = set()
+
+    def bind_dense(self, coord, W, act=-1, dtype=1, bias=None):
+        W = np.ascontiguousarray(W, np.float32)
+        raw, scale = self.O.pack(dtype, W)
+        self.cells[tuple(coord)] = dict(dtype=dtype, act=act, raw=raw, scale=scale,
+                                        out=W.shape[0], inn=W.shape[1],
+                                        bias=None if bias is None else np.asarray(bias, np.float64))
+
+    def set_remote_link(self, coord, target):
+        self.remote[tuple(coord)] = tuple(target)
+
+    def set_disabled(self, coord, disabled=True):
+        (self.disabled.add if disabled else self.disabled.discard)(tuple(coord))
+
+    def weights(self, coord) -> np.ndarray:
+        c = self.cells[tuple(coord)]
+        return self.O.decode_f64(c["dtype"], c["raw"], c["scale"],
+                                 c["out"] * c["inn"]).reshape(c["out"], c["inn"])
+
+    def export_f32(self, coord) -> np.ndarray:
+        c = self.cells[tuple(coord)]
+        return self.O.decode(c["dtype"], c["raw"], c["scale"],
+                             c["out"] * c["inn"]).reshape(c["out"], c["inn"])
+
+    def hop_order(self):
+        D, R, Cc, L = self.dims
+        for z in range(D):
+            for y in range(R):
+                for x in range(Cc):
+                    for l in range(L):
+                        yield (z, y, x, l)
+
+    def forward(self, x):
+        """-> (code, message, y, tape); tape = [(coord, input, pre, post)]."""
+        cur = np.ascontiguousarray(x, np.float32)
+        posts, tape = {}, []
+        for co in self.hop_order():
+            if co in self.disabled:
+                continue
+            if co not in self.cells:
+                return 1, "runtime.forward: no op at z=%d y=%d x=%d l=%d" % co, None, tape
+            inp = cur
+            if co in self.remote:
+                t = self.remote[co]
+                if t not in posts:
+                    return 1, "runtime.forward: remote hop has no recorded activation", None, tape
+                inp = posts[t]
+            c = self.cells[co]
+            if inp.shape[1] != c["inn"]:
+                return 1, "dense: input width mismatch", None, tape
+            pre, post = self.O.forward(self.weights(co), inp, c["act"], c["bias"])
+            tape.append((co, inp, pre, post))
+            posts[co] = post
+            cur = post
+        if not tape:
+            return 1, "runtime.forward: grid has no enabled cells with ops", None, tape
+        return 0, "", cur, tape
+
+    def train_step(self, x, target, lr):
+        """-> (code, message, loss, y)."""
+        code, msg, y, tape = self.forward(x)
+        if code:
+            return code, msg, 0.0, None
+        t = np.ascontiguousarray(target, np.float32)
+        if t.shape != y.shape:
+            return 1, "training: MSE shape", 0.0, y
+        loss = self.O.mse(y, t)
+        gy = self.O.mse_grad(y, t)
+        grads = {}
+        for co, inp, pre, _ in reversed(tape):
+            c = self.cells[co]
+            if gy.shape[1] != c["out"]:  # dense::backward_f32 shape check, dense.cpp:171-178
+                return 1, "dense: bwd shape mismatch", loss, y
+            _, dX, dW = self.O.backward(self.weights(co), inp, pre, gy, c["act"])
+            grads[co] = dW
+            gy = dX
+        if lr == 0.0:
+            return 1, "training: LR is 0", loss, y
+        if not np.isfinite(lr):
+            return 1, "weights: bad SGD arguments", loss, y
+        for co, _, _, _ in tape:
+            c = self.cells[co]
+            dW = grads[co]
+            if c["dtype"] == 1:  # Float32 launcher checks, training.mm:71-128
+                if not np.all(np.isfinite(dW)):
+                    return 2, "SGD: gradient is not a finite f32", loss, y
+                if abs(lr) > np.finfo(np.float32).max or abs(lr) < np.finfo(np.float32).tiny:
+                    return 2, "SGD: learning rate outside the f32 range", loss, y
+                w = c["raw"].view(np.float32)
+                self.O.sgd_f32(w, dW.ravel(), lr)
+            else:
+                st = self.O.native_sgd(c["dtype"], c["raw"], c["scale"], c["out"] * c["inn"],
+                                       dW, lr)
+                if st:
+                    return 1, "weights: nonfinite gradient", loss, y
+        return 0, "", loss, y

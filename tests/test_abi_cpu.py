@@ -49,6 +49,9 @@ def test_no_device_is_unsupported():
     with pytest.raises(pywelvet.WelvetError) as e:
         pywelvet.init()
     assert e.value.code == 2
+    with pytest.raises(pywelvet.WelvetError) as e:
+        pywelvet.Grid(1, 1, 1, 1, 1)
+    assert e.value.code == 2
 
 
 def test_argument_errors_before_device():
@@ -69,3 +72,7 @@ def test_argument_errors_before_device():
     assert r["status"].code == 1  # c_abi.cpp:155-160
     r = pywelvet.normalbp(np.eye(2), np.ones((0, 2)), np.zeros((0, 2)), 1, 0.1, status=True)
     assert r["status"].code == 1
+    h = ctypes.c_void_p()
+    assert L.welvet_hip_grid_new(1, 1, 1, 1, 0, ctypes.byref(h)).code == 1  # batch <= 0
+    assert L.welvet_hip_grid_new(1, 1, 1, 1, 1, None).code == 1
+    assert L.welvet_hip_volume_forward(None, None, 0, None, 0).code == 1

@@ -1,0 +1,196 @@
+"""GPU volume runtime against the oracle's volume restatement: hop order,
+remote links, disabled cells, error messages, and training steps
+(MSE, reverse backward, SGD with re-encode) on multi-cell grids."""
+import numpy as np
+import pytest
+
+import pywelvet
+from oracle import Volume
+from parity import assert_close, rel_err, tol_for_k
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    pywelvet.init()
+
+
+def build(oracle, dims, batch, spec, remote=(), disabled=()):
+    """spec: {coord: (W, act, dtype, bias)} -> (GPU grid, oracle volume)."""
+    G = pywelvet.Grid(*dims, batch)
+    V = Volume(oracle, *dims, batch)
+    for co, (W, act, dt, bias) in spec.items():
+        G.bind_dense(co, W, act=act, dtype=dt, bias=bias)
+        V.bind_dense(co, W, act=act, dtype=dt, bias=bias)
+    for co, t in remote:
+        G.set_remote_link(co, t)
+        V.set_remote_link(co, t)
+    for co in disabled:
+        G.set_disabled(co)
+        V.set_disabled(co)
+    return G, V
+
+
+def test_c1_single_cell_tanh(oracle):
+    """Config 1: 1x1x1 volume, Dense 512->512 Float32, batch 1, tanh,
+    W ~ U(-0.05, 0.05), x ~ N(0, 1)."""
+    rng = np.random.default_rng(0x5EED0000)
+    W = rng.uniform(-0.05, 0.05, (512, 512)).astype(np.float32)
+    x = rng.normal(0, 1, (1, 512)).astype(np.float32)
+    G, V = build(oracle, (1, 1, 1, 1), 1, {(0, 0, 0, 0): (W, 3, 1, None)})
+    with G:
+        y = G.forward(x, 512)
+    code, _, ry, _ = V.forward(x)
+    assert code == 0
+    assert_close(y, ry, 512, "c1")
+
+
+def _stack_spec(rng, dims, width, dtypes, acts=None):
+    spec = {}
+    coords = [(z, yy, xx, l) for z in range(dims[0]) for yy in range(dims[1])
+              for xx in range(dims[2]) for l in range(dims[3])]
+    for i, co in enumerate(coords):
+        W = rng.normal(0, 1.0 / np.sqrt(width), (width, width)).astype(np.float32)
+        act = (acts[i] if acts else (0 if i < len(coords) - 1 else -1))
+        bias = rng.normal(0, 0.1, width) if i % 3 == 0 else None
+        spec[co] = (W, act, dtypes[i % len(dtypes)], bias)
+    return spec
+
+
+def test_forward_2x2x2x4_mixed_dtypes(oracle):
+    rng = np.random.default_rng(5)
+    dtypes = [1, 4, 26, 9, 16, 2, 3, 5, 14, 0, 27, 13]
+    spec = _stack_spec(rng, (2, 2, 2, 4), 128, dtypes)
+    G, V = build(oracle, (2, 2, 2, 4), 16, spec)
+    x = rng.normal(0, 1, (16, 128)).astype(np.float32)
+    with G:
+        y = G.forward(x, 128)
+    code, _, ry, _ = V.forward(x)
+    assert code == 0
+    # 32 chained layers, each within the 1e-5 per-layer bound: 1e-5 per layer
+    e = rel_err(y, ry)
+    assert e <= 32 * 1e-5, e
+
+
+def test_remote_link_disabled_and_widths(oracle):
+    rng = np.random.default_rng(6)
+    spec = {(0, 0, 0, 0): (rng.normal(0, 0.3, (24, 16)), 0, 4, None),
+            (0, 0, 1, 0): (rng.normal(0, 0.3, (12, 24)), 1, 26, rng.normal(0, 1, 12)),
+            (0, 0, 2, 0): (rng.normal(0, 0.3, (8, 24)), 3, 9, None),
+            (0, 0, 3, 0): (rng.normal(0, 0.3, (8, 8)), -1, 1, None)}
+    G, V = build(oracle, (1, 1, 5, 1), 3, spec, remote=[((0, 0, 2, 0), (0, 0, 0, 0))],
+                 disabled=[(0, 0, 4, 0)])
+    x = rng.normal(0, 1, (3, 16)).astype(np.float32)
+    with G:
+        y = G.forward(x, 8)
+        code, _, ry, _ = V.forward(x)
+        assert code == 0
+        assert_close(y, ry, 24, "remote")
+
+
+def test_forward_errors_match_oracle(oracle):
+    rng = np.random.default_rng(7)
+    W = rng.normal(0, 0.3, (4, 4)).astype(np.float32)
+    x = np.ones((1, 4), np.float32)
+    with pywelvet.Grid(1, 1, 2, 1, 1) as G:
+        G.bind_dense((0, 0, 0, 0), W)
+        st, _ = G.forward(x, 4, status=True)
+        assert st.code == 1 and st.message.decode().startswith("runtime.forward: no op at z=0 y=0 x=1")
+        G.set_disabled((0, 0, 1, 0))
+        assert G.forward(x, 4).shape == (1, 4)
+        st, _ = G.forward(np.ones((1, 5), np.float32), 4, status=True)
+        assert (st.code, st.message.decode()) == (1, "dense: input width mismatch")
+        st = G.bind_dense((0, 0, 2, 0), W, status=True)
+        assert st.code == 1 and st.message.decode() == "architecture: bad bind coord z=0 y=0 x=2 l=0"
+        st = G.set_remote_link((0, 0, 0, 0), (0, 0, 9, 0), status=True)
+        assert st.code == 1 and "bad target coord" in st.message.decode()
+        st = G.bind_dense((0, 0, 1, 0), W, dtype=34, status=True)
+        assert st.code == 2
+    with pywelvet.Grid(1, 1, 2, 1, 1) as G:
+        G.bind_dense((0, 0, 0, 0), W)
+        G.bind_dense((0, 0, 1, 0), W)
+        G.set_remote_link((0, 0, 0, 0), (0, 0, 1, 0))
+        st, _ = G.forward(x, 4, status=True)
+        assert st.code == 1 and "remote hop has no recorded activation" in st.message.decode()
+
+
+def _check_weights(G, V, spec, label):
+    """After SGD the stored weights agree with the oracle's up to what the
+    forward/backward tolerance allows in dW: Float32/Float64 stores within a
+    few ulp (lr*dW is far below one ulp of the weight's error budget); coded
+    stores identical except where fl32(old - lr*g) sat within that error of a
+    rounding boundary — at most 1% of elements, each by about one code step."""
+    for co, (_, _, dtype, _) in spec.items():
+        a, b = G.export_f32(co), V.export_f32(co)
+        if dtype in (0, 1):
+            # a few ulp of the matrix's largest weight: the error of lr*dW is
+            # absolute, not relative to each weight
+            atol = 4 * float(np.spacing(np.float32(np.abs(b).max())))
+            np.testing.assert_allclose(a, b, rtol=4e-7, atol=atol, err_msg=f"{label} {co}")
+            continue
+        diff = a != b
+        assert diff.mean() <= 1e-2, (label, co, diff.mean())
+        if diff.any():
+            step = np.abs(a[diff] - b[diff])
+            span = np.abs(b).max() + 1e-30
+            assert np.all(step <= max(span * 0.3, 1e-6)), (label, co, step.max())
+
+
+@pytest.mark.parametrize("dtypes", [[1], [4, 9], [26, 1, 16], [2, 3, 5, 14]],
+                         ids=["f32", "fp8-int8", "nf4-f32-fp4", "mixed"])
+def test_train_steps_match_oracle(oracle, dtypes):
+    rng = np.random.default_rng(11 + len(dtypes))
+    dims = (1, 2, 2, 2)
+    spec = _stack_spec(rng, dims, 64, dtypes)
+    G, V = build(oracle, dims, 8, spec)
+    x = rng.normal(0, 1, (8, 64)).astype(np.float32)
+    t = rng.normal(0, 1, (8, 64)).astype(np.float32)
+    with G:
+        for step in range(3):
+            loss, y = G.train_step(x, t, 1e-2)
+            code, _, rloss, ry = V.train_step(x, t, 1e-2)
+            assert code == 0
+            # 8 chained layers: 1e-5 relative per layer
+            assert rel_err(y, ry) <= 8 * 1e-5, (step, rel_err(y, ry))
+            assert abs(loss - rloss) <= 8 * 1e-5 * abs(rloss), (step, loss, rloss)
+            _check_weights(G, V, spec, f"step {step}")
+            # re-sync the oracle to the GPU's stored bytes so later steps
+            # compare one step each, not an accumulated drift
+            for co in spec:
+                raw, _ = G.native(co)
+                V.cells[co]["raw"] = raw.copy()
+
+
+def test_step_errors_match_oracle(oracle):
+    rng = np.random.default_rng(13)
+    W = rng.normal(0, 0.3, (4, 4)).astype(np.float32)
+    x = rng.normal(0, 1, (2, 4)).astype(np.float32)
+    for dtype, nan_code, nan_msg in ((9, 1, "weights: nonfinite gradient"),
+                                     (1, 2, "SGD: gradient is not a finite f32")):
+        with pywelvet.Grid(1, 1, 2, 1, 2) as G:
+            G.bind_dense((0, 0, 0, 0), W, act=0, dtype=dtype)
+            G.bind_dense((0, 0, 1, 0), W, dtype=dtype)
+            before = [G.export_f32((0, 0, i, 0)) for i in range(2)]
+            st, _, _ = G.train_step(x, np.zeros((2, 4)), 0.0, status=True)
+            assert (st.code, st.message.decode()) == (1, "training: LR is 0")
+            st, _, _ = G.train_step(x, np.zeros((2, 3)), 0.1, status=True)
+            assert (st.code, st.message.decode()) == (1, "training: MSE shape")
+            t = np.zeros((2, 4), np.float32)
+            t[1, 2] = np.nan
+            st, _, _ = G.train_step(x, t, 0.1, status=True)
+            assert (st.code, st.message.decode()) == (nan_code, nan_msg)
+            for i in range(2):
+                np.testing.assert_array_equal(G.export_f32((0, 0, i, 0)), before[i])
+    with pywelvet.Grid(1, 1, 2, 1, 1) as G:
+        G.bind_dense((0, 0, 0, 0), W, dtype=1)
+        G.bind_dense((0, 0, 1, 0), W, dtype=1)
+        st, _, _ = G.train_step(x[:1], np.zeros((1, 4)), 1e300, status=True)
+        assert (st.code, st.message.decode()) == (2, "SGD: learning rate outside the f32 range")
+    with pywelvet.Grid(1, 1, 3, 1, 1) as G:
+        G.bind_dense((0, 0, 0, 0), rng.normal(0, 1, (3, 4)))
+        G.bind_dense((0, 0, 1, 0), rng.normal(0, 1, (5, 3)))
+        G.bind_dense((0, 0, 2, 0), rng.normal(0, 1, (2, 3)))
+        G.set_remote_link((0, 0, 2, 0), (0, 0, 0, 0))
+        st, _, _ = G.train_step(np.ones((1, 4)), np.zeros((1, 2)), 0.1, status=True)
+        assert (st.code, st.message.decode()) == (1, "dense: bwd shape mismatch")

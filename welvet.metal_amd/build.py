@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libwelvet_hip.so")
-SOURCES = ["codec.hip", "dense.hip", "runtime.cpp"]
+SOURCES = ["codec.hip", "dense.hip", "runtime.cpp", "volume.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -191,7 +191,8 @@ __device__ inline float sgd_value(uint64_t code, int64_t i, float g, double lr, 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body, int64_t n,
                                                        const float *__restrict__ g, double lr,
-                                                       float scale, float minv) {
+                                                       float scale, float minv, const int *stop) {
+  if (stop != nullptr && *stop != 0) return;
   constexpr int bits = dtype_bits(DT);
   constexpr int U = unit_elems<DT>();
   const int64_t units = (n + U - 1) / U;
@@ -233,7 +234,9 @@ __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ bod
 // Float64 storage keeps full f64: w = w - lr*g (native_codec.cpp:933-939
 // pinned to the f64 value its soft-double approximates).
 __global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ w, int64_t n,
-                                                           const float *__restrict__ g, double lr) {
+                                                           const float *__restrict__ g, double lr,
+                                                           const int *stop) {
+  if (stop != nullptr && *stop != 0) return;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads)
     w[i] = w[i] - lr * (double)g[i];
@@ -242,7 +245,9 @@ __global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ 
 // welvet_sgd_f32_f64_grad welvet_dense.metal:263-281: the step is rounded to
 // f32 first, then subtracted in f32.
 __global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w, int64_t n,
-                                                           const float *__restrict__ g, double lr) {
+                                                           const float *__restrict__ g, double lr,
+                                                           const int *stop) {
+  if (stop != nullptr && *stop != 0) return;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads) {
     const float step = (float)(lr * (double)g[i]);
@@ -250,13 +255,15 @@ __global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w
   }
 }
 
+// flag := value when g holds a non-finite element and flag is still 0 (the
+// first failing check of a sequence keeps its value).
 __global__ void __launch_bounds__(kThreads) nonfinite_kernel(const float *__restrict__ g, int64_t n,
-                                                             int *flag) {
+                                                             int *flag, int value) {
   int bad = 0;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads)
     bad |= !isfinite(g[i]);
-  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicCAS(flag, 0, value);
 }
 
 }  // namespace
@@ -315,19 +322,19 @@ hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s
 }
 
 hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double lr, float scale,
-                      float minv, hipStream_t s) {
+                      float minv, const int *stop, hipStream_t s) {
   if (dt == kFloat32) {
-    sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr);
+    sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop);
     return hipGetLastError();
   }
   if (dt == kFloat64) {
-    sgd_f64_kernel<<<grid_for(n), kThreads, 0, s>>>((double *)body, n, g, lr);
+    sgd_f64_kernel<<<grid_for(n), kThreads, 0, s>>>((double *)body, n, g, lr, stop);
     return hipGetLastError();
   }
 #define WH_SGD(D)                                                                           \
   if constexpr (D != kFloat32 && D != kFloat64) {                                           \
     sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
-        body, n, g, lr, scale, minv);                                                       \
+        body, n, g, lr, scale, minv, stop);                                                 \
     return hipGetLastError();                                                               \
   } else {                                                                                  \
     return hipErrorInvalidValue;                                                            \
@@ -336,8 +343,8 @@ hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double l
 #undef WH_SGD
 }
 
-hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, hipStream_t s) {
-  nonfinite_kernel<<<grid_for(n / 4 + 1), kThreads, 0, s>>>(g, n, flag);
+hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s) {
+  nonfinite_kernel<<<grid_for(n / 4 + 1), kThreads, 0, s>>>(g, n, flag, value);
   return hipGetLastError();
 }
 

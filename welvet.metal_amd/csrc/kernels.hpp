@@ -35,9 +35,11 @@ hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta 
 hipError_t launch_decode(int dt, const uint8_t *body, int64_t n, float scale, float minv, float *out,
                          hipStream_t s);
 hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s);
+// SGD with fixed-scale re-encode; a no-op when `stop` is non-null and *stop != 0.
 hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double lr, float scale,
-                      float minv, hipStream_t s);
-hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, hipStream_t s);
+                      float minv, const int *stop, hipStream_t s);
+// *flag = value if g holds a non-finite element and *flag is still 0.
+hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s);
 
 // ---- dense.hip
 // Bytes of workspace the forward / backward launches below need.

@@ -20,12 +20,13 @@
 #include <string>
 
 #include "../../include/welvet_c.h"
-#include "codec.hpp"
-#include "kernels.hpp"
+#include "runtime.hpp"
 
 using namespace wh;
+using namespace wh::rt;
 
-namespace {
+namespace wh {
+namespace rt {
 
 welvet_status make_status(int code, const char *fmt, ...) {
   welvet_status st{};
@@ -36,14 +37,8 @@ welvet_status make_status(int code, const char *fmt, ...) {
   va_end(ap);
   return st;
 }
-welvet_status ok() { return welvet_status{}; }
 
-#define WH_HIP(expr)                                                                   \
-  do {                                                                                 \
-    hipError_t e_ = (expr);                                                            \
-    if (e_ != hipSuccess)                                                              \
-      return make_status(kInternal, "hip: %s at %s:%d", hipGetErrorString(e_), __FILE__, __LINE__); \
-  } while (0)
+
 
 // ------------------------------------------------------------ device state
 struct Device {
@@ -88,26 +83,17 @@ welvet_status require_device() {
   return ok();
 }
 
+bool device_ready() {
+  device_init();
+  return g_dev.status == kOk;
+}
+
+const char *device_identity() {
+  device_init();
+  return g_dev.identity.c_str();
+}
+
 // ------------------------------------------------------- resident store
-struct Store {
-  int dtype = kFloat32, rows = 0, cols = 0;
-  float scale = 1.0f, minv = 0.0f;
-  uint8_t *body = nullptr;  // payload without the unsigned header
-  size_t body_bytes = 0;    // payload bytes in the reference layout minus header
-  float *lut = nullptr;
-  double *bias = nullptr;
-  int bias_len = 0;
-
-  float tab16[16] = {};  // host copy of the first 16 decoded table values
-
-  DevStore dev() const {
-    DevStore d{dtype, rows, cols, scale, minv, body, lut, {}};
-    for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
-    return d;
-  }
-  int64_t n() const { return (int64_t)rows * cols; }
-};
-
 void free_store(Store *w) {
   if (w->body) (void)hipFree(w->body);
   if (w->lut) (void)hipFree(w->lut);
@@ -192,7 +178,7 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
   if (n > INT32_MAX) return make_status(kInvalid, "SGD: tensor too large");
   int flag = 0;
   WH_HIP(hipMemsetAsync(d_flag, 0, sizeof(int), s));
-  WH_HIP(launch_nonfinite(d_dW, n, d_flag, s));
+  WH_HIP(launch_nonfinite(d_dW, n, d_flag, 1, s));
   WH_HIP(hipMemcpyAsync(&flag, d_flag, sizeof(int), hipMemcpyDeviceToHost, s));
   WH_HIP(hipStreamSynchronize(s));
   if (w->dtype == kFloat32) {
@@ -202,7 +188,7 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
   } else if (flag) {
     return make_status(kInvalid, "weights: nonfinite gradient");
   }
-  WH_HIP(launch_sgd(w->dtype, w->body, n, d_dW, lr, w->scale, w->minv, s));
+  WH_HIP(launch_sgd(w->dtype, w->body, n, d_dW, lr, w->scale, w->minv, nullptr, s));
   return ok();
 }
 
@@ -227,7 +213,8 @@ bool dims_ok(int32_t rows, int32_t cols) {
   return rows > 0 && cols > 0 && (int64_t)rows * cols <= INT32_MAX;
 }
 
-}  // namespace
+}  // namespace rt
+}  // namespace wh
 
 // ------------------------------------------------------------- session
 struct welvet_dense_session {

@@ -1,0 +1,65 @@
+// runtime.hpp — host-side pieces shared by the Dense session runtime and
+// the volume runtime: status helpers, device bring-up and the resident
+// packed weight store.  Internal to the library (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/welvet_c.h"
+#include "codec.hpp"
+#include "kernels.hpp"
+
+namespace wh {
+namespace rt {
+
+welvet_status make_status(int code, const char *fmt, ...);
+inline welvet_status ok() { return welvet_status{}; }
+
+#define WH_HIP(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return make_status(kInternal, "hip: %s at %s:%d", hipGetErrorString(e_), __FILE__, __LINE__); \
+  } while (0)
+
+// Brings up device 0 once (gfx950 only); code 2 when unusable.
+welvet_status require_device();
+void device_init();
+bool device_ready();
+const char *device_identity();
+
+// ------------------------------------------------------- resident store
+struct Store {
+  int dtype = kFloat32, rows = 0, cols = 0;
+  float scale = 1.0f, minv = 0.0f;
+  uint8_t *body = nullptr;  // payload without the unsigned header
+  size_t body_bytes = 0;    // payload bytes in the reference layout minus header
+  float *lut = nullptr;
+  double *bias = nullptr;
+  int bias_len = 0;
+
+  float tab16[16] = {};  // host copy of the first 16 decoded table values
+
+  DevStore dev() const {
+    DevStore d{dtype, rows, cols, scale, minv, body, lut, {}};
+    for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
+    return d;
+  }
+  int64_t n() const { return (int64_t)rows * cols; }
+};
+
+void free_store(Store *w);
+// WeightStore::make on the device from f32 values already in HBM.
+welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d_w, hipStream_t s);
+welvet_status store_set_bias(Store *w, const double *bias, size_t bias_len, hipStream_t s);
+welvet_status store_from_host(Store *w, int dtype, int rows, int cols, const float *W_init,
+                              hipStream_t s);
+// WeightStore::apply_sgd with a device gradient; synchronises to check it.
+welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hipStream_t s);
+welvet_status store_native(const Store &w, uint8_t *out, size_t cap, size_t *len, hipStream_t s);
+welvet_status store_export(const Store &w, float *d_out, hipStream_t s);
+bool dims_ok(int32_t rows, int32_t cols);
+
+}  // namespace rt
+}  // namespace wh

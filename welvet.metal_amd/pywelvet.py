@@ -97,6 +97,30 @@ def lib() -> C.CDLL:
         L.welvet_hip_set_forward_path.restype = None
         L.welvet_hip_set_tuning.argtypes = [_i32, _i32]
         L.welvet_hip_set_tuning.restype = _i32
+        coord = [_vp] + [_i32] * 4
+        L.welvet_hip_grid_new.argtypes = [_i32] * 5 + [C.POINTER(_vp)]
+        L.welvet_hip_grid_new.restype = Status
+        L.welvet_hip_grid_release.argtypes = [_vp]
+        L.welvet_hip_grid_release.restype = None
+        L.welvet_hip_grid_bind_dense.argtypes = coord + [_i32] * 4 + [_f, _d, C.c_size_t]
+        L.welvet_hip_grid_bind_dense.restype = Status
+        L.welvet_hip_grid_set_remote_link.argtypes = coord + [_i32] * 4
+        L.welvet_hip_grid_set_remote_link.restype = Status
+        L.welvet_hip_grid_set_disabled.argtypes = coord + [_i32]
+        L.welvet_hip_grid_set_disabled.restype = Status
+        L.welvet_hip_volume_forward.argtypes = [_vp, _f, _i32, _f, _i32]
+        L.welvet_hip_volume_forward.restype = Status
+        L.welvet_hip_volume_forward_device.argtypes = [_vp, _vp, _i32, _vp, _i32, _vp]
+        L.welvet_hip_volume_forward_device.restype = Status
+        L.welvet_hip_volume_train_step.argtypes = [_vp, _f, _i32, _f, _i32, C.c_double, _d, _f]
+        L.welvet_hip_volume_train_step.restype = Status
+        L.welvet_hip_volume_train_step_device.argtypes = [_vp, _vp, _i32, _vp, _i32, C.c_double,
+                                                          _d, _vp]
+        L.welvet_hip_volume_train_step_device.restype = Status
+        L.welvet_hip_grid_export_f32.argtypes = coord + [_f]
+        L.welvet_hip_grid_export_f32.restype = Status
+        L.welvet_hip_grid_native.argtypes = coord + [_u8, C.c_size_t, C.POINTER(C.c_size_t), _f]
+        L.welvet_hip_grid_native.restype = Status
         _LIB = L
     return _LIB
 
@@ -255,3 +279,87 @@ def mse(pred, target):
     g = np.zeros(p.size, np.float32)
     check(lib().welvet_hip_mse_f32(_fp(p), _fp(t), p.size, C.byref(loss), _fp(g)))
     return loss.value, g
+
+
+class Grid:
+    """The volume runtime: architecture::Grid with Dense cells, volume forward
+    and training::step_dense (welvet_hip_grid_* / welvet_hip_volume_*)."""
+
+    def __init__(self, depth, rows, cols, layers, batch):
+        h = _vp()
+        check(lib().welvet_hip_grid_new(depth, rows, cols, layers, batch, C.byref(h)))
+        self.h = h
+        self.batch = batch
+        self.widths = {}
+
+    def close(self):
+        if self.h:
+            lib().welvet_hip_grid_release(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def bind_dense(self, coord, W, act=-1, dtype=1, bias=None, status=False):
+        W = _f32(W)
+        out, inn = W.shape
+        b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+        st = lib().welvet_hip_grid_bind_dense(self.h, *coord, inn, out, act, dtype, _fp(W), _dp(b),
+                                              0 if b is None else b.size)
+        if status:
+            return st
+        check(st)
+        self.widths[tuple(coord)] = (inn, out)
+
+    def set_remote_link(self, coord, target, status=False):
+        st = lib().welvet_hip_grid_set_remote_link(self.h, *coord, *target)
+        if status:
+            return st
+        check(st)
+
+    def set_disabled(self, coord, disabled=True):
+        check(lib().welvet_hip_grid_set_disabled(self.h, *coord, int(disabled)))
+
+    def forward(self, x, out, status=False):
+        x = _f32(x)
+        y = np.zeros((self.batch, out), np.float32)
+        st = lib().welvet_hip_volume_forward(self.h, _fp(x), x.shape[-1], _fp(y), out)
+        if status:
+            return st, y
+        check(st)
+        return y
+
+    def train_step(self, x, target, lr, status=False):
+        x, t = _f32(x), _f32(target)
+        y = np.zeros(t.shape, np.float32)
+        loss = C.c_double()
+        st = lib().welvet_hip_volume_train_step(self.h, _fp(x), x.shape[-1], _fp(t), t.shape[-1],
+                                                lr, C.byref(loss), _fp(y))
+        if status:
+            return st, loss.value, y
+        check(st)
+        return loss.value, y
+
+    def export_f32(self, coord):
+        inn, out = self.widths[tuple(coord)]
+        W = np.zeros((out, inn), np.float32)
+        check(lib().welvet_hip_grid_export_f32(self.h, *coord, _fp(W)))
+        return W
+
+    def native(self, coord):
+        n = C.c_size_t()
+        s = C.c_float()
+        lib().welvet_hip_grid_native(self.h, *coord, None, 0, C.byref(n), C.byref(s))
+        out = np.zeros(n.value, np.uint8)
+        check(lib().welvet_hip_grid_native(self.h, *coord, out.ctypes.data_as(_u8), out.size,
+                                           C.byref(n), C.byref(s)))
+        return out, s.value
