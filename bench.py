@@ -133,6 +133,155 @@ def cpu_baseline(dtype: int, batch: int, seconds: float = 12.0):
                           "sample": f"{msteps} full steps ({mt:.1f} s), OpenMP over rows"}}
 
 
+# ---------------------------------------------------------------- configs
+# The other BASELINE configurations, reported under "config_results" (they
+# are not the headline metric).  Weights are seeded per config and layer.
+
+
+def _weights(rng, out, inn, init):
+    import numpy as np
+    if init == "uniform05":
+        return rng.uniform(-0.05, 0.05, (out, inn)).astype(np.float32)
+    if init == "uniform6":
+        return rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+    return (rng.standard_normal((out, inn), dtype=np.float32) * np.float32(0.02))
+
+
+def _grid(P, widths, dtype, batch, rng, init, act_hidden=-1, act_out=-1, shared=None):
+    """A 1 x 1 x L x 1 grid of Dense cells widths[0] -> ... -> widths[-1]."""
+    L = len(widths) - 1
+    g = P.Grid(1, 1, L, 1, batch)
+    for l in range(L):
+        key = (widths[l], widths[l + 1])
+        if shared is not None and key in shared:
+            W = shared[key]
+        else:
+            W = _weights(rng, widths[l + 1], widths[l], init)
+            if shared is not None:
+                shared[key] = W
+        g.bind_dense((0, 0, l, 0), W, act=act_hidden if l < L - 1 else act_out, dtype=dtype)
+    return g
+
+
+def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, init="normal"):
+    """Forward of a Dense chain on device buffers; rotates grid copies so the
+    working set exceeds the MALL."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    bits = P.dtype_bits(dtype)
+    wbytes = sum(widths[i] * widths[i + 1] * bits // 8 for i in range(len(widths) - 1))
+    copies = max(2, -(-MALL_BYTES // wbytes))
+    shared = {}
+    grids = [_grid(P, widths, dtype, batch, rng, init, shared=shared) for _ in range(copies)]
+    dev = torch.device("cuda:0")
+    x = torch.randn((batch, widths[0]), device=dev)
+    y = torch.empty((batch, widths[-1]), device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    sh = stream.cuda_stream
+
+    def step(i):
+        P.check(P.lib().welvet_hip_volume_forward_device(
+            grids[i % copies].h, x.data_ptr(), widths[0], y.data_ptr(), widths[-1], sh))
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    for g in grids:
+        g.close()
+    flops = 2.0 * batch * sum(widths[i] * widths[i + 1] for i in range(len(widths) - 1))
+    return {"widths": widths, "weight_dtype": P.DTYPE_NAMES[dtype], "batch": batch, "init": init,
+            "packed_bytes": wbytes, "weight_copies": copies, "ms_per_step": ms,
+            "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
+
+
+def time_volume_train(torch, P, dims, widths, dtype, batch, steps, seed, lr=1e-3):
+    """training::step_dense on device buffers (forward, MSE vs N(0,1) targets,
+    backward, SGD with re-encode); one synchronisation per step."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    D, R, Cc, L = dims
+    g = P.Grid(D, R, Cc, L, batch)
+    n_layers = 0
+    for z in range(D):
+        for yy in range(R):
+            for xx in range(Cc):
+                for l in range(L):
+                    k = n_layers
+                    W = _weights(rng, widths[k + 1], widths[k], "normal")
+                    last = k == len(widths) - 2
+                    g.bind_dense((z, yy, xx, l), W, act=-1 if last else 0, dtype=dtype)
+                    n_layers += 1
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(rng.standard_normal((batch, widths[0]), dtype=np.float32)).to(dev)
+    t = torch.from_numpy(rng.standard_normal((batch, widths[-1]), dtype=np.float32)).to(dev)
+    stream = torch.cuda.Stream(device=dev)
+    loss = P.C.c_double()
+    codes = []
+
+    def step():
+        st = P.lib().welvet_hip_volume_train_step_device(
+            g.h, x.data_ptr(), widths[0], t.data_ptr(), widths[-1], lr, P.C.byref(loss),
+            stream.cuda_stream)
+        # a non-finite gradient (a diverging deep quantized stack) is the
+        # reference's own error: the step ran, SGD was skipped; report it
+        if st.code not in (0, 1, 2) or (st.code and b"nonfinite" not in st.message
+                                          and b"finite f32" not in st.message):
+            P.check(st)
+        codes.append(st.code)
+
+    torch.cuda.synchronize()
+    step()  # first step allocates dW and gradient buffers
+    first_loss = loss.value
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    g.close()
+    mac = sum(widths[i] * widths[i + 1] for i in range(len(widths) - 1))
+    return {"widths": widths if len(widths) < 8 else f"{len(widths) - 1} x {widths[1]}",
+            "weight_dtype": P.DTYPE_NAMES[dtype], "batch": batch, "steps": steps, "lr": lr,
+            "ms_per_step": ms, "tflops": 6.0 * batch * mac / (ms * 1e-3) / 1e12,
+            "loss_first": first_loss, "loss_last": loss.value,
+            "sgd_skipped_nonfinite": sum(1 for c in codes if c)}
+
+
+def run_configs(torch, P):
+    """BASELINE configs 2-5 (config 1 is the reference's own CPU case)."""
+    out = {}
+    seed = 0x5EED0000
+    for name, dt in (("e4m3", 4), ("e5m2", 5)):
+        for b in (1, 32):
+            out[f"c2_{name}_4096x4096_b{b}"] = time_volume_forward(
+                torch, P, [4096, 4096], dt, b, 100, 10, seed + 1)
+    for name, dt, init in (("nf4", 26, "normal"), ("fp4", 16, "normal"), ("fp4_u6", 16, "uniform6")):
+        for b in (1, 8, 64):
+            out[f"c3_{name}_4096-11008-4096_b{b}"] = time_volume_forward(
+                torch, P, [4096, 11008, 4096], dt, b, 50, 5, seed + 2, init=init)
+    for name, dt in (("int8", 9), ("e4m3", 4)):
+        out[f"c4_{name}_2048-8192-2048_b256"] = time_volume_train(
+            torch, P, (1, 1, 2, 1), [2048, 8192, 2048], dt, 256, 10, seed + 3)
+    c5, skipped = {}, []
+    for dt in range(34):
+        r = time_volume_train(torch, P, (2, 2, 2, 4), [1024] * 33, dt, 16, 2, seed + 4)
+        c5[P.DTYPE_NAMES[dt]] = round(r["ms_per_step"], 4)
+        if r["sgd_skipped_nonfinite"]:
+            skipped.append(P.DTYPE_NAMES[dt])
+    out["c5_2x2x2x4_1024_b16_ms_per_step"] = c5
+    out["c5_nonfinite_gradient_dtypes"] = skipped
+    for k, v in out.items():
+        if isinstance(v, dict) and "ms_per_step" in v:
+            print(f"# {k}: {v['ms_per_step'] * 1e3:.1f} us/step  {v.get('tflops', 0):.2f} TFLOP/s",
+                  file=sys.stderr, flush=True)
+    return out
+
+
 def calibrate_copy(torch, mib: int = 256, launches: int = 5):
     """Element-wise copy out = in * 1 of `mib` MiB, `launches` times: each launch
     reads and writes exactly mib MiB, the yardstick for FETCH_SIZE/WRITE_SIZE."""
@@ -160,6 +309,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of cases: fp8b1,nf4b1,fp8b64,nf4b64")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip BASELINE configs 2-5 (reported under config_results)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (for scaling HBM counters)")
     a = ap.parse_args()
@@ -210,6 +361,8 @@ def main():
         "results": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},
     }
+    if not a.no_configs:
+        line["config_results"] = run_configs(torch, pywelvet)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(prim["weight_dtype"] == "nf4" and 26 or 4, prim["batch"])
     print(json.dumps(line), flush=True)

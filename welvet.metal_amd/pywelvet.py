@@ -24,6 +24,13 @@ DTYPE_NAMES = [
     "fp6", "int6", "uint6", "int5", "uint5", "int3", "uint3",
 ]
 DTYPE = {n: i for i, n in enumerate(DTYPE_NAMES)}
+# bits per element of each dtype's native code (include/welvet/dtype.hpp order)
+DTYPE_BITS = [64, 32, 16, 16, 8, 8, 64, 32, 16, 8, 64, 32, 16, 8, 4, 4, 4, 2, 2, 2, 1, 64, 64, 64,
+              64, 128, 4, 6, 6, 6, 5, 5, 3, 3]
+
+
+def dtype_bits(dtype: int) -> int:
+    return DTYPE_BITS[dtype]
 ACT = {"linear": -1, "relu": 0, "silu": 1, "gelu": 2, "tanh": 3, "sigmoid": 4, "leakyrelu": 5,
        "relu2": 6}
 
