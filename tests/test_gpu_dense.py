@@ -67,7 +67,9 @@ def test_forward_each_route(oracle, dtype, path):
 KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24), dict(cr=1),
          dict(cr=2), dict(cr=3), dict(cr=4), dict(reg_gemm=0), dict(gemm_occ=4),
          dict(fast_decode=0, pair_lut=0), dict(fast_decode=1), dict(pair_lut=1),
-         dict(fast_decode=1, pair_lut=1, gemv1=0), dict(fast_decode=1, pair_lut=1, reg_gemm=0)]
+         dict(fast_decode=1, pair_lut=1, gemv1=0), dict(fast_decode=1, pair_lut=1, reg_gemm=0),
+         dict(gemv_rows=1), dict(gemv_rows=2), dict(gemv_rows=4), dict(gemv_rows=2, cr=1),
+         dict(gemv_rows=1, cr=2), dict(gemv_rows=1, pair_lut=0, fast_decode=0)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -143,8 +145,8 @@ def test_session_reuse(oracle):
 
 @pytest.mark.parametrize("dtype", [4, 26, 1])
 def test_gemm_session_repeat(oracle, dtype):
-    """Repeated MFMA launches on one session: the stream-K tile counters the
-    GEMMs leave behind must let every later forward and dX come out right."""
+    """Repeated MFMA launches on one session reuse its stream-K workspace:
+    every later forward and dX must come out right."""
     rng = np.random.default_rng(17 + dtype)
     out, inn, batch = 1500, 2048, 48
     W = rng.normal(0, 0.05, (out, inn)).astype(np.float32)

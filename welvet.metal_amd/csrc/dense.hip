@@ -80,6 +80,9 @@ struct FI {
   static constexpr int kE = kBits <= 6 ? 32 : 128 / kBits;
   static constexpr int kW = kBits <= 6 ? kBits : 4;
   using Acc = std::conditional_t<F == FF64, double, float>;
+  // decodes that can be Inf or NaN (float codes; 8-bit tables include E5M2)
+  static constexpr bool kMayBeNonFinite = F == FE5 || F == FL8 || F == FH16 || F == FB16 ||
+                                          F == FF32 || F == FF64 || F == FC64 || F == FC128;
 };
 
 // Fills the block's LDS table from the store's 2^bits decoded values.
@@ -439,33 +442,50 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
   const int cbase = wave * 64 * C + lane;
   // issue order matters: vmcnt retires in order, so the table and x loads go
   // first and row r's arithmetic waits only for loads up to row r
+  // Loads are unconditional, from clamped in-range addresses (lanes past the
+  // row end or rows past N read a valid chunk whose products are never
+  // used): straight-line loads let each row's arithmetic wait for exactly
+  // the loads before it instead of for all of them.
   float xv[C][E];
 #pragma unroll
   for (int cc = 0; cc < C; ++cc) {
-    const int c = cbase + cc * 64;
-    if (c < a.nchunks) load_x<E>(a.x + (int64_t)c * E, xv[cc]);
-    else {
-#pragma unroll
-      for (int e = 0; e < E; ++e) xv[cc][e] = 0.0f;
-    }
+    const int c = min(cbase + cc * 64, a.nchunks - 1);
+    load_x<E>(a.x + (int64_t)c * E, xv[cc]);
   }
   uint32_t w[R][C][W];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = min(r0 + r, a.N - 1);
 #pragma unroll
     for (int cc = 0; cc < C; ++cc) {
-      const int c = cbase + cc * 64;
-      if (r0 + r < a.N && c < a.nchunks)
-        load_words<W>(a.body + (int64_t)(r0 + r) * a.row_bytes + (int64_t)c * (W * 4), w[r][cc]);
-      else {
-#pragma unroll
-        for (int i = 0; i < W; ++i) w[r][cc][i] = 0;
-      }
+      const int c = min(cbase + cc * 64, a.nchunks - 1);
+      load_words<W>(a.body + row * a.row_bytes + (int64_t)c * (W * 4), w[r][cc]);
     }
+  }
   if constexpr (I::kLut && F != FL4 && F != FL4P) {
     if (tid < NL) lut_s[tid] = lut_v;
     for (int i = tid + blockDim.x; i < NL; i += blockDim.x) lut_s[i] = a.lut[i];
     __syncthreads();
+  }
+  // A wave whose column slice runs past the row end zeroes, on its lanes
+  // past the end (duplicate reads), x and — for formats with non-finite
+  // codes — the weight words, so they add exact zeros.  The lane mask is
+  // opaque to the compiler, which would otherwise move the loads under a
+  // branch on it (and then wait for all of them at the join).
+  if (__builtin_amdgcn_readfirstlane(wave) * 64 * C + 64 * C > a.nchunks) {
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) {
+      uint32_t keep = cbase + cc * 64 < a.nchunks ? ~0u : 0u;
+      asm volatile("" : "+v"(keep));
+#pragma unroll
+      for (int e = 0; e < E; ++e) xv[cc][e] = __uint_as_float(__float_as_uint(xv[cc][e]) & keep);
+      if constexpr (FI<F>::kMayBeNonFinite) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int i = 0; i < W; ++i) w[r][cc][i] &= keep;
+      }
+    }
   }
   double acc[R];
 #pragma unroll
@@ -473,12 +493,10 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
     Acc s[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int cc = 0; cc < C; ++cc) {
-      if (cbase + cc * 64 < a.nchunks) {
-        Acc v[E];
-        decode_chunk<F>(w[r][cc], v, lut_s, a.scale, a.minv);
+      Acc v[E];
+      decode_chunk<F>(w[r][cc], v, lut_s, a.scale, a.minv);
 #pragma unroll
-        for (int e = 0; e < E; ++e) s[e & 3] = fma(v[e], (Acc)xv[cc][e], s[e & 3]);
-      }
+      for (int e = 0; e < E; ++e) s[e & 3] = fma(v[e], (Acc)xv[cc][e], s[e & 3]);
     }
     acc[r] = ((double)s[0] + (double)s[1]) + ((double)s[2] + (double)s[3]);
   }
@@ -529,13 +547,6 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
   }
 }
 
-// Batch-1 GEMV, persistent and software-pipelined: a fixed number of waves
-// (a few per CU) each hold their x chunks in registers for the whole kernel
-// (one wave covers a row's C*64 chunks) and walk row groups of R rows strided
-// by the wave count.  The next group's R*C weight chunks are loaded while the
-// current group is decoded and multiplied, so HBM streams continuously and
-// the VALU work overlaps it; each group ends with a butterfly reduction whose
-// owning lanes store the rows.
 // Element-wise fallback for shapes whose rows do not start on a chunk
 // boundary: a block per output row, f64 accumulation, any batch.
 template <int DT>
@@ -1043,7 +1054,7 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0};
 
 inline int blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
@@ -1053,6 +1064,12 @@ inline int blocks_for(int64_t n) {
 bool chunk_aligned(const DevStore &w, int64_t len) {
   const int f = fmt_of(w.dtype);
   return f >= 0 && len % fmt_chunk_elems(f) == 0;
+}
+
+// Formats whose batch-1 GEMV takes the rows-per-block knob.
+constexpr bool gemv_rows_knob(int f) {
+  return f == FE4 || f == FE5 || f == FI8 || f == FL4P || f == FL4 || f == FL8 || f == FH16 ||
+         f == FB16;
 }
 
 // Kernel format of a dtype under the current knobs.
@@ -1217,9 +1234,22 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       }
       const int S = (a.nchunks + 64 * C - 1) / (64 * C);
       if (S <= 4) {
-        const int R = 8 / C;
+        // rows per block: 8 / C, or the knob's 1, 2, 4 or 8 (at most 8 / C)
+        // for the formats the sweeps cover
+        int R = 8 / C;
+        const int rk = g_tune[kTuneGemvRows];
+        if ((rk == 1 || rk == 2 || rk == 4 || rk == 8) && rk <= R && gemv_rows_knob(f)) R = rk;
         const int blocks = (a.N + R - 1) / R;
 #define WH_PF(F)                                                                         \
+  if constexpr (gemv_rows_knob(F)) {                                                     \
+    if (C == 1 && R == 1) gemv_pf_kernel<F, 1, 1><<<blocks, 64 * S, 0, s>>>(a);          \
+    else if (C == 1 && R == 2) gemv_pf_kernel<F, 1, 2><<<blocks, 64 * S, 0, s>>>(a);     \
+    else if (C == 1 && R == 4) gemv_pf_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);     \
+    else if (C == 2 && R == 1) gemv_pf_kernel<F, 2, 1><<<blocks, 64 * S, 0, s>>>(a);     \
+    else if (C == 2 && R == 2) gemv_pf_kernel<F, 2, 2><<<blocks, 64 * S, 0, s>>>(a);     \
+    else if (C == 4 && R == 1) gemv_pf_kernel<F, 4, 1><<<blocks, 64 * S, 0, s>>>(a);     \
+    if (R < 8 / C) return hipGetLastError();                                             \
+  }                                                                                      \
   if (C == 1) gemv_pf_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a);                      \
   else if (C == 2) gemv_pf_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a);                 \
   else if (C == 4) gemv_pf_kernel<F, 4, 2><<<blocks, 64 * S, 0, s>>>(a);                 \
