@@ -172,7 +172,8 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *   6 hardware FP8 conversions and integer Int8 decode instead of tables [1]
  *   7 byte-pair decode table for 4-bit formats [1]
  *   8 all-loads-in-flight rows per block: 0 = 8 / chunks per lane, or 1, 2,
- *     4, 8 (FP8, Int8, 4-bit, 8-bit table and half formats) [0] */
+ *     4, 8, 16 (at most 16 / chunks per lane; FP8, Int8, 4-bit, 8-bit table
+ *     and half formats) [0] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

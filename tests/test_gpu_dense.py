@@ -69,7 +69,8 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(fast_decode=0, pair_lut=0), dict(fast_decode=1), dict(pair_lut=1),
          dict(fast_decode=1, pair_lut=1, gemv1=0), dict(fast_decode=1, pair_lut=1, reg_gemm=0),
          dict(gemv_rows=1), dict(gemv_rows=2), dict(gemv_rows=4), dict(gemv_rows=2, cr=1),
-         dict(gemv_rows=1, cr=2), dict(gemv_rows=1, pair_lut=0, fast_decode=0)]
+         dict(gemv_rows=1, cr=2), dict(gemv_rows=1, pair_lut=0, fast_decode=0),
+         dict(gemv_rows=16, cr=3), dict(gemv_rows=8, cr=1), dict(gemv_rows=16, cr=3, pair_lut=0)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -94,6 +95,26 @@ def test_forward_kernel_variants(oracle, knobs):
                 _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, 0)
                 assert_close(dX, rdX, 96, "dX")
                 assert_bit_equal(dW, rdW, "dW")
+    finally:
+        for k, v in old.items():
+            pywelvet.set_tuning(k, v)
+
+
+def test_every_gemv_shape_knob_launches(oracle):
+    """Every (chunks per lane, rows per block) request, including ones with
+    no kernel of their own, computes the forward (falls back, never skips)."""
+    rng = np.random.default_rng(23)
+    cases = [(4, 300, 1024), (26, 257, 2048), (9, 64, 4096), (2, 40, 3072)]
+    old = {k: pywelvet.set_tuning(k, 0) for k in ("cr", "gemv_rows")}
+    try:
+        for cr in range(5):
+            for rows in (0, 1, 2, 3, 4, 8, 16, 32):
+                pywelvet.set_tuning("cr", cr)
+                pywelvet.set_tuning("gemv_rows", rows)
+                for dtype, out, inn in cases:
+                    W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+                    x = rng.normal(0, 1, (1, inn)).astype(np.float32)
+                    check_forward(oracle, dtype, W, x)
     finally:
         for k, v in old.items():
             pywelvet.set_tuning(k, v)

@@ -503,31 +503,17 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
   // butterfly over the R rows: after log2(R) exchange steps on lane bits
   // 5, 4, ... lane l holds a partial of row (l >> (6 - log2 R)); the
   // remaining xor steps finish the 64-lane sum.
-  double v;
-  if constexpr (R == 1) {
-    v = acc[0];
-  } else if constexpr (R == 2) {
-    const int b5 = (lane >> 5) & 1;
-    v = (b5 ? acc[1] : acc[0]) + __shfl_xor(b5 ? acc[0] : acc[1], 32);
-  } else if constexpr (R == 4) {
-    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1;
-    double t[2];
+  constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
+  static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      t[i] = (b5 ? acc[i + 2] : acc[i]) + __shfl_xor(b5 ? acc[i] : acc[i + 2], 32);
-    v = (b4 ? t[1] : t[0]) + __shfl_xor(b4 ? t[0] : t[1], 16);
-  } else {  // R == 8
-    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1, b3 = (lane >> 3) & 1;
-    double t4[4], t2[2];
+  for (int k = 0; k < LR; ++k) {
+    const int half = R >> (k + 1), bit = 5 - k;
+    const bool hi = (lane >> bit) & 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      t4[i] = (b5 ? acc[i + 4] : acc[i]) + __shfl_xor(b5 ? acc[i] : acc[i + 4], 32);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      t2[i] = (b4 ? t4[i + 2] : t4[i]) + __shfl_xor(b4 ? t4[i] : t4[i + 2], 16);
-    v = (b3 ? t2[1] : t2[0]) + __shfl_xor(b3 ? t2[0] : t2[1], 8);
+    for (int i = 0; i < half; ++i)
+      acc[i] = (hi ? acc[i + half] : acc[i]) + __shfl_xor(hi ? acc[i] : acc[i + half], 1 << bit);
   }
-  constexpr int LR = R == 1 ? 0 : (R == 2 ? 1 : (R == 4 ? 2 : 3));
+  double v = acc[0];
 #pragma unroll
   for (int off = 32 >> LR; off > 0; off >>= 1) v += __shfl_xor(v, off);
   const int S = blockDim.x >> 6;
@@ -1072,6 +1058,13 @@ constexpr bool gemv_rows_knob(int f) {
          f == FB16;
 }
 
+// (chunks per lane, rows per block) shapes of the all-loads GEMV built in
+// addition to the default (C, 8 / C).
+constexpr bool gemv_pf_extra(int C, int R) {
+  return (C == 1 && (R == 1 || R == 2 || R == 4 || R == 16)) ||
+         (C == 2 && (R == 1 || R == 2 || R == 8)) || (C == 4 && R == 1);
+}
+
 // Kernel format of a dtype under the current knobs.
 int kernel_fmt(int dt) {
   const int f = fmt_of(dt);
@@ -1222,8 +1215,12 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
                row_bytes_of(w), bias, bias_len, act, pre, post, {}};
     for (int i = 0; i < 16; ++i) a.tab16[i] = w.tab16[i];
     if (batch == 1 && g_tune[kTuneGemv1] == 1) {
-      // (C, R): chunks per lane and rows per block, C*R = 8 loads per lane
-      int C = 1;
+      // (C, R): chunks per lane and rows per block.  Auto: the fewest chunks
+      // per lane that cover a row with at most 4 waves, and 8 / C rows; for
+      // FP8 / Int8 rows of one chunk per lane and for 4-bit rows that two
+      // chunks per lane cover, 4 rows (measured best: more blocks in flight
+      // for the heavier FP8 decode, one wave per block for 4-bit)
+      int C = 1, Rauto = 0;
       switch (g_tune[kTuneCR]) {
       case 1: C = 2; break;
       case 2: C = 4; break;
@@ -1231,24 +1228,31 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       case 4: C = 8; break;
       default:
         while (C < 8 && (a.nchunks + 64 * C - 1) / (64 * C) > 4) C *= 2;
+        if ((f == FE4 || f == FE5 || f == FI8) && C == 1) Rauto = 4;
+        if ((f == FL4P || f == FL4) && a.nchunks <= 128) C = 2, Rauto = 4;
       }
       const int S = (a.nchunks + 64 * C - 1) / (64 * C);
       if (S <= 4) {
-        // rows per block: 8 / C, or the knob's 1, 2, 4 or 8 (at most 8 / C)
-        // for the formats the sweeps cover
+        // rows per block: 8 / C, or the knob's value (else the auto choice)
+        // where that (C, R) kernel exists (the formats the sweeps cover)
         int R = 8 / C;
-        const int rk = g_tune[kTuneGemvRows];
-        if ((rk == 1 || rk == 2 || rk == 4 || rk == 8) && rk <= R && gemv_rows_knob(f)) R = rk;
+        const int rk = g_tune[kTuneGemvRows] ? g_tune[kTuneGemvRows] : Rauto;
+        if (gemv_rows_knob(f) && gemv_pf_extra(C, rk)) R = rk;
         const int blocks = (a.N + R - 1) / R;
 #define WH_PF(F)                                                                         \
   if constexpr (gemv_rows_knob(F)) {                                                     \
-    if (C == 1 && R == 1) gemv_pf_kernel<F, 1, 1><<<blocks, 64 * S, 0, s>>>(a);          \
-    else if (C == 1 && R == 2) gemv_pf_kernel<F, 1, 2><<<blocks, 64 * S, 0, s>>>(a);     \
-    else if (C == 1 && R == 4) gemv_pf_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);     \
-    else if (C == 2 && R == 1) gemv_pf_kernel<F, 2, 1><<<blocks, 64 * S, 0, s>>>(a);     \
-    else if (C == 2 && R == 2) gemv_pf_kernel<F, 2, 2><<<blocks, 64 * S, 0, s>>>(a);     \
-    else if (C == 4 && R == 1) gemv_pf_kernel<F, 4, 1><<<blocks, 64 * S, 0, s>>>(a);     \
-    if (R < 8 / C) return hipGetLastError();                                             \
+    if (R != 8 / C) {                                                                    \
+      if (C == 1 && R == 1) gemv_pf_kernel<F, 1, 1><<<blocks, 64 * S, 0, s>>>(a);        \
+      else if (C == 1 && R == 2) gemv_pf_kernel<F, 1, 2><<<blocks, 64 * S, 0, s>>>(a);   \
+      else if (C == 1 && R == 4) gemv_pf_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);   \
+      else if (C == 1 && R == 16) gemv_pf_kernel<F, 1, 16><<<blocks, 64 * S, 0, s>>>(a); \
+      else if (C == 2 && R == 1) gemv_pf_kernel<F, 2, 1><<<blocks, 64 * S, 0, s>>>(a);   \
+      else if (C == 2 && R == 2) gemv_pf_kernel<F, 2, 2><<<blocks, 64 * S, 0, s>>>(a);   \
+      else if (C == 2 && R == 8) gemv_pf_kernel<F, 2, 8><<<blocks, 64 * S, 0, s>>>(a);   \
+      else if (C == 4 && R == 1) gemv_pf_kernel<F, 4, 1><<<blocks, 64 * S, 0, s>>>(a);   \
+      else return hipErrorInvalidValue;                                                  \
+      return hipGetLastError();                                                          \
+    }                                                                                    \
   }                                                                                      \
   if (C == 1) gemv_pf_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a);                      \
   else if (C == 2) gemv_pf_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a);                 \

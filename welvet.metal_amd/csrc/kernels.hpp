@@ -73,7 +73,7 @@ void set_forward_path(int path);
 // per CU (0 = 2).
 // 6 hardware FP8 converts / integer Int8 decode instead of tables (1 on),
 // 7 pair table for 4-bit formats (1 on).
-// 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8).
+// 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kNumTune = 9
