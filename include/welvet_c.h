@@ -173,7 +173,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *   7 byte-pair decode table for 4-bit formats [1]
  *   8 all-loads-in-flight rows per block: 0 = 8 / chunks per lane, or 1, 2,
  *     4, 8, 16 (at most 16 / chunks per lane; FP8, Int8, 4-bit, 8-bit table
- *     and half formats) [0] */
+ *     and half formats) [0]
+ *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
+ *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2, else 0) [-1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

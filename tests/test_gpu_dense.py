@@ -70,7 +70,9 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(fast_decode=1, pair_lut=1, gemv1=0), dict(fast_decode=1, pair_lut=1, reg_gemm=0),
          dict(gemv_rows=1), dict(gemv_rows=2), dict(gemv_rows=4), dict(gemv_rows=2, cr=1),
          dict(gemv_rows=1, cr=2), dict(gemv_rows=1, pair_lut=0, fast_decode=0),
-         dict(gemv_rows=16, cr=3), dict(gemv_rows=8, cr=1), dict(gemv_rows=16, cr=3, pair_lut=0)]
+         dict(gemv_rows=16, cr=3), dict(gemv_rows=8, cr=1), dict(gemv_rows=16, cr=3, pair_lut=0),
+         dict(gemv_waves=0), dict(gemv_waves=1), dict(gemv_waves=12), dict(gemv_waves=1, cr=1),
+         dict(gemv_waves=2, gemv_rows=16, cr=3), dict(gemv_waves=1, gemv_rows=1, pair_lut=0)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -162,6 +164,27 @@ def test_session_reuse(oracle):
             pre, post = s.execute(x)
             rpre, rpost = oracle.forward(Wd, x, 3)
             assert_close(post, rpost, 512, f"iter {i}")
+
+
+@pytest.mark.parametrize("dtype", [4, 5])
+@pytest.mark.parametrize("batch", [1, 8, 64])
+def test_forward_after_sgd_reads_updated_store(oracle, dtype, batch):
+    """FP8 kernels decode the store's decode-ready copy: after an SGD step
+    (which rewrites both) the forward must match the oracle on the exported
+    weights, including codes the update moved into or out of the subnormal
+    range (decoded as signed zero)."""
+    rng = np.random.default_rng(40 + dtype + batch)
+    out, inn = 260, 1024
+    W = rng.normal(0, 0.02, (out, inn)).astype(np.float32)
+    with pywelvet.Session(W, batch=batch, act=-1, dtype=dtype) as s:
+        for step in range(2):
+            g = rng.normal(0, 1, (out, inn)).astype(np.float32)
+            s.sgd(g, 5e-3)
+            Wd = s.export_f32().astype(np.float64)
+            x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+            pre, _ = s.execute(x)
+            rpre, _ = oracle.forward(Wd, x, -1)
+            assert_close(pre, rpre, inn, f"{DTYPE_NAMES[dtype]} step {step}")
 
 
 @pytest.mark.parametrize("dtype", [4, 26, 1])

@@ -127,6 +127,7 @@ __global__ void finalize_kernel(const float *__restrict__ w, const Stats *acc, M
 template <int DT>
 __global__ void __launch_bounds__(kThreads) pack_kernel(const float *__restrict__ w, int64_t n,
                                                         uint8_t *__restrict__ body,
+                                                        uint8_t *__restrict__ kbody,
                                                         const Meta *__restrict__ meta) {
   constexpr int bits = dtype_bits(DT);
   constexpr int U = unit_elems<DT>();
@@ -136,6 +137,7 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const float *__restrict_
        u += (int64_t)gridDim.x * kThreads) {
     if constexpr (bits >= 8) {
       const uint64_t c = pack_code<DT>(w[u], m);
+      if constexpr (has_kcopy<DT>()) kbody[u] = kcode<DT>((uint32_t)c);
       if constexpr (bits == 8) body[u] = (uint8_t)c;
       else if constexpr (bits == 16) ((uint16_t *)body)[u] = (uint16_t)c;
       else if constexpr (bits == 32) ((uint32_t *)body)[u] = (uint32_t)c;
@@ -189,7 +191,8 @@ __device__ inline float sgd_value(uint64_t code, int64_t i, float g, double lr, 
 }
 
 template <int DT>
-__global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body, int64_t n,
+__global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body,
+                                                       uint8_t *__restrict__ kbody, int64_t n,
                                                        const float *__restrict__ g, double lr,
                                                        float scale, float minv, const int *stop) {
   if (stop != nullptr && *stop != 0) return;
@@ -202,6 +205,7 @@ __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ bod
       const uint64_t c = fix_code<DT>(sgd_value<DT>(load_code<DT>(body, u), u, g[u], lr, scale, minv),
                                       scale, minv);
       constexpr int fb = fix_bytes<DT>();
+      if constexpr (has_kcopy<DT>()) kbody[u] = kcode<DT>((uint32_t)c);
       if constexpr (fb == 1) body[u] = (uint8_t)c;
       else if constexpr (fb == 2) ((uint16_t *)body)[u] = (uint16_t)c;
       else if constexpr (fb == 4) ((uint32_t *)(body + u * (bits / 8)))[0] = (uint32_t)c;
@@ -283,9 +287,10 @@ __global__ void __launch_bounds__(kThreads) nonfinite_kernel(const float *__rest
   default: return hipErrorInvalidValue;                                                           \
   }
 
-hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta *meta, Stats *stats,
-                         hipStream_t s) {
+hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, uint8_t *kbody, Meta *meta,
+                         Stats *stats, hipStream_t s) {
   if (n <= 0) return hipErrorInvalidValue;
+  if ((dt == kFP8E4M3 || dt == kFP8E5M2) && kbody == nullptr) return hipErrorInvalidValue;
   stats_init_kernel<<<1, 1, 0, s>>>(stats);
   int sblocks = grid_for(n / 4 + 1);
   if (sblocks > 1024) sblocks = 1024;
@@ -293,7 +298,7 @@ hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta 
 #define WH_ENC(D)                                                                      \
   finalize_kernel<D><<<1, 1, 0, s>>>(w, stats, meta);                                  \
   pack_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
-      w, n, body, meta);                                                               \
+      w, n, body, kbody, meta);                                                        \
   return hipGetLastError();
   WH_DTYPE_SWITCH(dt, WH_ENC)
 #undef WH_ENC
@@ -321,8 +326,9 @@ hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s
 #undef WH_LUT
 }
 
-hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double lr, float scale,
-                      float minv, const int *stop, hipStream_t s) {
+hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
+                      float scale, float minv, const int *stop, hipStream_t s) {
+  if ((dt == kFP8E4M3 || dt == kFP8E5M2) && kbody == nullptr) return hipErrorInvalidValue;
   if (dt == kFloat32) {
     sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop);
     return hipGetLastError();
@@ -334,7 +340,7 @@ hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double l
 #define WH_SGD(D)                                                                           \
   if constexpr (D != kFloat32 && D != kFloat64) {                                           \
     sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
-        body, n, g, lr, scale, minv, stop);                                                 \
+        body, kbody, n, g, lr, scale, minv, stop);                                          \
     return hipGetLastError();                                                               \
   } else {                                                                                  \
     return hipErrorInvalidValue;                                                            \

@@ -194,6 +194,27 @@ __host__ __device__ constexpr int unit_elems() {
   return b >= 8 ? 1 : (b == 1 || b == 2 || b == 4 ? 8 / b : 8);
 }
 
+// Decode-ready copy of an FP8 code: the byte the hardware converters
+// (v_cvt_*_fp8 / _bf8, OCP formats) decode to exactly the reference's value.
+// E4M3 (float_codecs.cpp:99-117): a zero exponent field decodes to signed
+// zero, 0x7f / 0xff decode to +-448 (= 0x7e / 0xfe; OCP reads 0x7f as NaN).
+// E5M2 (:160-181): a zero exponent field decodes to signed zero; Inf and NaN
+// codes already agree.  Stores keep the reference bytes (export, SGD); kernels
+// that decode FP8 through the converters read this copy.
+template <int DT>
+__host__ __device__ constexpr bool has_kcopy() {
+  return DT == kFP8E4M3 || DT == kFP8E5M2;
+}
+template <int DT>
+__host__ __device__ inline uint8_t kcode(uint32_t c) {
+  if constexpr (DT == kFP8E4M3) {
+    if ((c & 0x78u) == 0) return (uint8_t)(c & 0x80u);
+    return (uint8_t)((c & 0x7fu) == 0x7fu ? c ^ 1u : c);
+  } else {
+    return (uint8_t)((c & 0x7cu) == 0 ? (c & 0x80u) : c);
+  }
+}
+
 // Reads the code of element i of a packed body.
 template <int DT>
 __device__ inline uint64_t load_code(const uint8_t *body, int64_t i) {

@@ -220,7 +220,10 @@ __device__ inline uint32_t nearest16(const float *tab, float r) {
 __device__ inline double sigmoid64(double x) { return 1.0 / (1.0 + exp(-x)); }
 __device__ inline double tanh64(double x) { return x > 18 ? 1.0 : (x < -18 ? -1.0 : tanh(x)); }
 
-__device__ inline float act_value(float v, int act) {
+// The activations that need exp/tanh, out of line: inlined into a
+// grid-stride kernel their f64 constants would be hoisted into registers for
+// the kernel's whole life.
+static __device__ __attribute__((noinline)) float act_value_f64(float v, int act) {
   const double x = (double)v;
   switch (act) {
   case kSilu: return (float)(x * sigmoid64(x));
@@ -231,9 +234,16 @@ __device__ inline float act_value(float v, int act) {
     const double u = (x + cubic) * 0.7978845608028654;
     return (float)((x * 0.5) * (1.0 + tanh64(u)));
   }
+  }
+  return v;
+}
+
+__device__ inline float act_value(float v, int act) {
+  switch (act) {
+  case kSilu: case kTanh: case kSigmoid: case kGELU: return act_value_f64(v, act);
   case kReLU: return v > 0.0f ? v : 0.0f;
   case kReLU2: return v < 0 ? 0.0f : v * v;
-  case kLeakyReLU: return v < 0 ? (float)(x * 0.01) : v;
+  case kLeakyReLU: return v < 0 ? (float)((double)v * 0.01) : v;
   }
   return v;
 }

@@ -22,6 +22,7 @@
 // Accumulation is fp32 inside a lane/tile and f64 across split-K / segment
 // partials; outputs are fl32 of that, within the stated tolerance of the f64
 // contract.  Float64 storage accumulates in f64 on the GEMV path.
+#include <algorithm>
 #include <type_traits>
 
 #include "codec.hpp"
@@ -33,9 +34,9 @@ namespace {
 // Kernel formats: dtypes sharing a body layout and decode share a kernel.
 // FL* decode through an LDS table of 2^bits exact values; FL4P is the 4-bit
 // layout read through a 256-entry table of value pairs (one read per byte);
-// FE4 / FE5 decode FP8 E4M3 / E5M2 with the hardware converts after a
-// 4-bytes-at-once fix-up to the reference's quirks; FI8 decodes Int8 by
-// integer conversion.
+// FE4 / FE5 decode FP8 E4M3 / E5M2 with the hardware converts, reading the
+// store's decode-ready copy (codec.hpp kcode: the reference's quirks applied
+// at encode / SGD time); FI8 decodes Int8 by integer conversion.
 enum Fmt {
   FL1, FL2, FL3, FL4, FL5, FL6, FL8, FH16, FB16, FI16, FU16, FF32, FI32, FU32, FI64, FU64, FC64,
   FC128, FF64, FE4, FE5, FI8, FL4P, kNumFmt
@@ -99,22 +100,6 @@ __device__ inline void fill_table(float *tab, const float *lut, int tid, int nth
   }
 }
 
-// Byte-wise fix-ups for the hardware FP8 converts (4 codes per word).
-// E4M3 (float_codecs.cpp:99-117): codes with a zero exponent field decode to
-// signed zero, and 0x7f decodes to 448 = 0x7e.  E5M2 (:160-181): zero
-// exponent field -> signed zero; Inf/NaN codes match the converter.
-__device__ inline uint32_t fix_e4m3_word(uint32_t w) {
-  const uint32_t nz = ((w & 0x78787878u) + 0x78787878u) & 0x80808080u;  // exponent != 0
-  const uint32_t keep = nz | (nz - (nz >> 7)) | 0x80808080u;
-  w &= keep;
-  const uint32_t is7f = (((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u) >> 7;
-  return w ^ is7f;
-}
-__device__ inline uint32_t fix_e5m2_word(uint32_t w) {
-  const uint32_t nz = ((w & 0x7c7c7c7cu) + 0x7c7c7c7cu) & 0x80808080u;
-  return w & (nz | (nz - (nz >> 7)) | 0x80808080u);
-}
-
 int fmt_chunk_elems(int f) {
   switch (f) {
   case FL1: case FL2: case FL3: case FL4: case FL5: case FL6: return 32;
@@ -151,6 +136,23 @@ __device__ inline void load_words(const uint8_t *__restrict__ p, uint32_t (&w)[W
   }
 }
 
+// load_words with the non-temporal hint (streamed weights, read once).
+template <int W>
+__device__ inline void load_words_nt(const uint8_t *__restrict__ p, uint32_t (&w)[W]) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+  if constexpr (W == 4) {
+    const u4v v = __builtin_nontemporal_load((const u4v *)p);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else if constexpr (W == 2) {
+    const u2v v = __builtin_nontemporal_load((const u2v *)p);
+    w[0] = v[0]; w[1] = v[1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = __builtin_nontemporal_load((const uint32_t *)p + i);
+  }
+}
+
 // Code of element e of a chunk (LSB-first bitstream over little-endian words).
 template <int BITS, int W>
 __device__ inline uint32_t chunk_code(const uint32_t (&w)[W], int e) {
@@ -171,7 +173,7 @@ __device__ inline typename FI<F>::Acc chunk_value(const uint32_t (&w)[FI<F>::kW]
     return lut[2 * b + (e & 1)];
   } else if constexpr (I::kLut) return lut[chunk_code<I::kBits, I::kW>(w, e)];
   else if constexpr (F == FE4 || F == FE5) {
-    const uint32_t q = F == FE4 ? fix_e4m3_word(w[e >> 2]) : fix_e5m2_word(w[e >> 2]);
+    const uint32_t q = w[e >> 2];
     f2 p;
     if (F == FE4) p = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_fp8(q, true) : __builtin_amdgcn_cvt_pk_f32_fp8(q, false);
     else p = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_bf8(q, true) : __builtin_amdgcn_cvt_pk_f32_bf8(q, false);
@@ -205,13 +207,11 @@ __device__ inline void decode_chunk(const uint32_t (&w)[FI<F>::kW], typename FI<
     for (int i = 0; i < 4; ++i) {
       f2 lo, hi;
       if constexpr (F == FE4) {
-        const uint32_t q = fix_e4m3_word(w[i]);
-        lo = __builtin_amdgcn_cvt_pk_f32_fp8(q, false);
-        hi = __builtin_amdgcn_cvt_pk_f32_fp8(q, true);
+        lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[i], false);
+        hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[i], true);
       } else {
-        const uint32_t q = fix_e5m2_word(w[i]);
-        lo = __builtin_amdgcn_cvt_pk_f32_bf8(q, false);
-        hi = __builtin_amdgcn_cvt_pk_f32_bf8(q, true);
+        lo = __builtin_amdgcn_cvt_pk_f32_bf8(w[i], false);
+        hi = __builtin_amdgcn_cvt_pk_f32_bf8(w[i], true);
       }
       v[4 * i] = lo[0];
       v[4 * i + 1] = lo[1];
@@ -531,6 +531,159 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
     for (int g = 0; g < S; ++g) s += part[g][tid];
     bias_act_store(s, r0 + tid, a.bias, a.bias_len, a.act, a.pre, a.post, r0 + tid);
   }
+}
+
+// gemv_pf_kernel as a grid-stride loop: a fixed number of blocks walks the
+// row groups, so x and the decode table are loaded once per block.  A row
+// group is R rows; the block's S waves split each row into column slices of 64*C
+// chunks (lane i of a wave reads chunk slice*64*C + cc*64 + i of each row:
+// 1 KB contiguous per wave per (row, cc)).  Per row group the lane issues all
+// R*C weight loads (non-temporal: the weights are streamed once) before any
+// arithmetic, so one memory latency covers the group.  Per-lane fp32 FMA over
+// its C*E products, then an f64 butterfly transpose-reduce over the R rows
+// and an ordered f64 sum over the S slices.  The block walks row groups
+// blockIdx.x, blockIdx.x + gridDim.x, ...
+template <int F, int C, int R>
+__global__ void __launch_bounds__(256) gemv_loop_kernel(GemvArgs a) {
+  using I = FI<F>;
+  using Acc = std::conditional_t<F == FF64, double, float>;
+  constexpr int E = I::kE, W = I::kW, NL = I::kTable;
+  constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
+  static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
+  __shared__ float lut_s[NL];
+  __shared__ double part[2][4][R];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int S = blockDim.x >> 6;
+  const int ngroups = (a.N + R - 1) / R;
+  float lut_v = 0.0f;
+  if constexpr (F == FL4 || F == FL4P) {
+    // the 16 decoded values come in the kernel arguments (scalar registers),
+    // so filling the LDS table waits for no vector load
+    for (int b = tid; b < (F == FL4 ? 16 : 256); b += blockDim.x) {
+      float lo = a.tab16[0], hi = a.tab16[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        lo = (b & 15) == i ? a.tab16[i] : lo;
+        hi = (b >> 4) == i ? a.tab16[i] : hi;
+      }
+      if constexpr (F == FL4) lut_s[b] = lo;
+      else {
+        lut_s[2 * b] = lo;
+        lut_s[2 * b + 1] = hi;
+      }
+    }
+    __syncthreads();
+  } else if constexpr (I::kLut) {
+    if (tid < NL) lut_v = a.lut[tid];
+  }
+  const int cbase = wave * 64 * C + lane;
+  // issue order matters: vmcnt retires in order, so the table and x loads go
+  // first and row r's arithmetic waits only for loads up to row r
+  // Loads are unconditional, from clamped in-range addresses (lanes past the
+  // row end or rows past N read a valid chunk whose products are never
+  // used): straight-line loads let each row's arithmetic wait for exactly
+  // the loads before it instead of for all of them.
+  float xv[C][E];
+#pragma unroll
+  for (int cc = 0; cc < C; ++cc) {
+    const int c = min(cbase + cc * 64, a.nchunks - 1);
+    load_x<E>(a.x + (int64_t)c * E, xv[cc]);
+  }
+  // A wave whose column slice runs past the row end zeroes, on its lanes
+  // past the end (duplicate reads), x and — for formats with non-finite
+  // codes — the weight words, so they add exact zeros.  The lane mask is
+  // opaque to the compiler, which would otherwise move the loads under a
+  // branch on it (and then wait for all of them at the join).
+  const bool ragged = __builtin_amdgcn_readfirstlane(wave) * 64 * C + 64 * C > a.nchunks;
+  uint32_t keep[C];
+#pragma unroll
+  for (int cc = 0; cc < C; ++cc) {
+    keep[cc] = cbase + cc * 64 < a.nchunks ? ~0u : 0u;
+    asm volatile("" : "+v"(keep[cc]));
+  }
+  // one row group: loads, decode + FMA, reductions, epilogue
+  auto group = [&](int g, bool first, int buf) {
+    const int r0 = g * R;
+    uint32_t w[R][C][W];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = min(r0 + r, a.N - 1);
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc) {
+        const int c = min(cbase + cc * 64, a.nchunks - 1);
+        const uint8_t *src = a.body + row * a.row_bytes + (int64_t)c * (W * 4);
+        load_words_nt<W>(src, w[r][cc]);
+      }
+    }
+    if (first) {
+      if constexpr (I::kLut && F != FL4 && F != FL4P) {
+        if (tid < NL) lut_s[tid] = lut_v;
+        for (int i = tid + blockDim.x; i < NL; i += blockDim.x) lut_s[i] = a.lut[i];
+        __syncthreads();
+      }
+      if (ragged) {
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc)
+#pragma unroll
+          for (int e = 0; e < E; ++e) xv[cc][e] = __uint_as_float(__float_as_uint(xv[cc][e]) & keep[cc]);
+      }
+    }
+    if constexpr (FI<F>::kMayBeNonFinite) {
+      if (ragged) {
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc)
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < W; ++i) w[r][cc][i] &= keep[cc];
+      }
+    }
+    double acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      Acc sm[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc) {
+        Acc v[E];
+        decode_chunk<F>(w[r][cc], v, lut_s, a.scale, a.minv);
+#pragma unroll
+        for (int e = 0; e < E; ++e) sm[e & 3] = fma(v[e], (Acc)xv[cc][e], sm[e & 3]);
+      }
+      acc[r] = ((double)sm[0] + (double)sm[1]) + ((double)sm[2] + (double)sm[3]);
+    }
+    // butterfly over the R rows: after log2(R) exchange steps on lane bits
+    // 5, 4, ... lane l holds a partial of row (l >> (6 - log2 R)); the
+    // remaining xor steps finish the 64-lane sum.
+#pragma unroll
+    for (int k = 0; k < LR; ++k) {
+      const int half = R >> (k + 1), bit = 5 - k;
+      const bool hi = (lane >> bit) & 1;
+#pragma unroll
+      for (int i = 0; i < half; ++i)
+        acc[i] = (hi ? acc[i + half] : acc[i]) + __shfl_xor(hi ? acc[i] : acc[i + half], 1 << bit);
+    }
+    double v = acc[0];
+#pragma unroll
+    for (int off = 32 >> LR; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (S == 1) {
+      if ((lane & ((64 >> LR) - 1)) == 0) {
+        const int row = r0 + (lane >> (6 - LR));
+        if (row < a.N) bias_act_store(v, row, a.bias, a.bias_len, a.act, a.pre, a.post, row);
+      }
+      return;
+    }
+    // part is double-buffered: the next group's writes go to the other half,
+    // and the barrier of that group orders them after this group's reads
+    if ((lane & ((64 >> LR) - 1)) == 0) part[buf][wave][lane >> (6 - LR)] = v;
+    __syncthreads();
+    if (tid < R && r0 + tid < a.N) {
+      double sum = 0;
+      for (int q = 0; q < S; ++q) sum += part[buf][q][tid];
+      bias_act_store(sum, r0 + tid, a.bias, a.bias_len, a.act, a.pre, a.post, r0 + tid);
+    }
+  };
+  int buf = 0;
+  for (int g = blockIdx.x; g < ngroups; g += gridDim.x, buf ^= 1) group(g, g == (int)blockIdx.x, buf);
 }
 
 // Element-wise fallback for shapes whose rows do not start on a chunk
@@ -1040,7 +1193,7 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1};
 
 inline int blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
@@ -1075,6 +1228,12 @@ int kernel_fmt(int dt) {
   }
   if (f == FL4 && g_tune[kTunePairLut]) return FL4P;
   return f;
+}
+
+// Payload a kernel format reads: the decode-ready copy for the formats
+// decoded by the FP8 converters (null when the store has none).
+const uint8_t *kernel_body(const DevStore &w, int f) {
+  return (f == FE4 || f == FE5) ? w.kbody : w.body;
 }
 
 int64_t row_bytes_of(const DevStore &w) {
@@ -1203,6 +1362,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
                           hipStream_t s) {
   const int route = fwd_route(w, batch);
   const int f = kernel_fmt(w.dtype);
+  if (kernel_body(w, f) == nullptr) return hipErrorInvalidValue;
   if (route == 3 || (route == 1 && batch > 4)) {
 #define WH_GEN(D)                                                                        \
   gemv_generic_kernel<D><<<w.rows, 256, 0, s>>>(w, batch, x, bias, bias_len, act, pre, post); \
@@ -1211,7 +1371,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
 #undef WH_GEN
   }
   if (route == 1) {
-    GemvArgs a{w.body, w.lut, w.scale, w.minv, x, w.cols, w.rows, w.cols / fmt_chunk_elems(f),
+    GemvArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, w.cols, w.rows, w.cols / fmt_chunk_elems(f),
                row_bytes_of(w), bias, bias_len, act, pre, post, {}};
     for (int i = 0; i < 16; ++i) a.tab16[i] = w.tab16[i];
     if (batch == 1 && g_tune[kTuneGemv1] == 1) {
@@ -1238,8 +1398,26 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         int R = 8 / C;
         const int rk = g_tune[kTuneGemvRows] ? g_tune[kTuneGemvRows] : Rauto;
         if (gemv_rows_knob(f) && gemv_pf_extra(C, rk)) R = rk;
-        const int blocks = (a.N + R - 1) / R;
+        // grid: one block per row group, or (knob / FP8 default) a fixed
+        // number of waves per CU walking the row groups, x loaded once each
+        // (the FP8 converter formats; others take one block per group)
+        const int ngroups = (a.N + R - 1) / R;
+        int wpc = g_tune[kTuneGemvWaves];
+        if (wpc < 0) wpc = (f == FE4 || f == FE5) ? 16 : 0;
+        int blocks = ngroups;
+        if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
 #define WH_PF(F)                                                                         \
+  if constexpr (F == FE4 || F == FE5) {                                                  \
+    if (blocks < ngroups) {                                                              \
+      if (C == 1 && R == 4) gemv_loop_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);  \
+      else if (C == 1 && R == 8) gemv_loop_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a); \
+      else if (C == 1 && R == 2) gemv_loop_kernel<F, 1, 2><<<blocks, 64 * S, 0, s>>>(a); \
+      else if (C == 2 && R == 4) gemv_loop_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a); \
+      else blocks = ngroups;                                                             \
+      if (blocks < ngroups) return hipGetLastError();                                    \
+    }                                                                                    \
+  }                                                                                      \
+  blocks = ngroups;                                                                      \
   if constexpr (gemv_rows_knob(F)) {                                                     \
     if (R != 8 / C) {                                                                    \
       if (C == 1 && R == 1) gemv_pf_kernel<F, 1, 1><<<blocks, 64 * S, 0, s>>>(a);        \
@@ -1283,7 +1461,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   }
   const SkPlan p = plan_fwd_gemm(f, batch, w.cols, w.rows);
   if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
-  GemmArgs a{w.body, w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
+  GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
              p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
   if (p.bn == kRegBN) {
 #define WH_GR(F)                                                                      \
@@ -1334,6 +1512,7 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   if (e != hipSuccess) return e;
   const int route = dx_route(w, batch);
   const int f = kernel_fmt(w.dtype);
+  if (kernel_body(w, f) == nullptr) return hipErrorInvalidValue;
   if (ws_bytes < backward_workspace_bytes(w, batch)) return hipErrorInvalidValue;
   if (route == 3) {
 #define WH_DXG(D)                                                                         \
@@ -1343,7 +1522,7 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
 #undef WH_DXG
   } else if (route == 1) {
     const int nseg = (w.rows + kDxSegRows - 1) / kDxSegRows;
-    DxArgs a{w.body, w.lut, w.scale, w.minv, dpre, w.rows, w.cols, w.cols / fmt_chunk_elems(f),
+    DxArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, w.rows, w.cols, w.cols / fmt_chunk_elems(f),
              kDxSegRows, nseg, row_bytes_of(w), (float *)ws};
     dim3 grid((a.nchunks + 255) / 256, nseg);
 #define WH_DXS(F)                                                  \
@@ -1358,7 +1537,7 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
         (const float *)ws, nseg, (int64_t)batch * w.cols, dX);
   } else {
     const SkPlan p = plan_sk(batch, w.rows, w.cols);
-    GemmArgs a{w.body, w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
+    GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
                p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
 #define WH_DXM(F)                                           \
   gemm_sk_kernel<F, true><<<p.blocks, 256, 0, s>>>(a);     \

@@ -25,19 +25,22 @@ struct DevStore {
   float scale;
   float minv;
   const uint8_t *body;
+  const uint8_t *kbody;  // FP8 formats: decode-ready copy of body (codec.hpp kcode)
   const float *lut;  // 2^bits decoded values for formats of <= 8 bits
   float tab16[16];   // host copy of the first 16 table values
 };
 
 // ---- codec.hip
-hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, Meta *meta, Stats *stats,
-                         hipStream_t s);
+// FP8 formats also write the decode-ready copy kbody (required for them).
+hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, uint8_t *kbody, Meta *meta,
+                         Stats *stats, hipStream_t s);
 hipError_t launch_decode(int dt, const uint8_t *body, int64_t n, float scale, float minv, float *out,
                          hipStream_t s);
 hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s);
 // SGD with fixed-scale re-encode; a no-op when `stop` is non-null and *stop != 0.
-hipError_t launch_sgd(int dt, uint8_t *body, int64_t n, const float *g, double lr, float scale,
-                      float minv, const int *stop, hipStream_t s);
+// FP8 formats also refresh the decode-ready copy kbody (required for them).
+hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
+                      float scale, float minv, const int *stop, hipStream_t s);
 // *flag = value if g holds a non-finite element and *flag is still 0.
 hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s);
 
@@ -74,9 +77,12 @@ void set_forward_path(int path);
 // 6 hardware FP8 converts / integer Int8 decode instead of tables (1 on),
 // 7 pair table for 4-bit formats (1 on).
 // 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
+// 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
+// block per row group; -1 = auto: 16 for the FP8 converter formats, else 0).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
-  kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kNumTune = 9
+  kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
+  kNumTune = 10
 };
 int set_tuning(int key, int value);
 

@@ -96,9 +96,11 @@ const char *device_identity() {
 // ------------------------------------------------------- resident store
 void free_store(Store *w) {
   if (w->body) (void)hipFree(w->body);
+  if (w->kbody) (void)hipFree(w->kbody);
   if (w->lut) (void)hipFree(w->lut);
   if (w->bias) (void)hipFree(w->bias);
   w->body = nullptr;
+  w->kbody = nullptr;
   w->lut = nullptr;
   w->bias = nullptr;
 }
@@ -122,6 +124,10 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
   const size_t alloc = ((w->body_bytes + 64 + 255) / 256) * 256;
   WH_HIP(hipMalloc(&w->body, alloc));
   WH_HIP(hipMemsetAsync(w->body, 0, alloc, s));
+  if (dtype == kFP8E4M3 || dtype == kFP8E5M2) {
+    WH_HIP(hipMalloc(&w->kbody, alloc));
+    WH_HIP(hipMemsetAsync(w->kbody, 0, alloc, s));
+  }
   if (dtype == kFloat32) {
     WH_HIP(hipMemcpyAsync(w->body, d_w, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
     w->scale = 1.0f;
@@ -130,7 +136,7 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
   }
   EncodeScratch *scratch = nullptr;
   WH_HIP(hipMalloc(&scratch, sizeof(EncodeScratch)));
-  hipError_t e = launch_encode(dtype, d_w, n, w->body, &scratch->meta, &scratch->stats, s);
+  hipError_t e = launch_encode(dtype, d_w, n, w->body, w->kbody, &scratch->meta, &scratch->stats, s);
   Meta m{};
   if (e == hipSuccess) e = hipMemcpyAsync(&m, &scratch->meta, sizeof(Meta), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -188,7 +194,7 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
   } else if (flag) {
     return make_status(kInvalid, "weights: nonfinite gradient");
   }
-  WH_HIP(launch_sgd(w->dtype, w->body, n, d_dW, lr, w->scale, w->minv, nullptr, s));
+  WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, s));
   return ok();
 }
 

@@ -34,6 +34,7 @@ struct Store {
   int dtype = kFloat32, rows = 0, cols = 0;
   float scale = 1.0f, minv = 0.0f;
   uint8_t *body = nullptr;  // payload without the unsigned header
+  uint8_t *kbody = nullptr; // FP8: decode-ready copy of body (same size), else null
   size_t body_bytes = 0;    // payload bytes in the reference layout minus header
   float *lut = nullptr;
   double *bias = nullptr;
@@ -42,7 +43,7 @@ struct Store {
   float tab16[16] = {};  // host copy of the first 16 decoded table values
 
   DevStore dev() const {
-    DevStore d{dtype, rows, cols, scale, minv, body, lut, {}};
+    DevStore d{dtype, rows, cols, scale, minv, body, kbody, lut, {}};
     for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
     return d;
   }

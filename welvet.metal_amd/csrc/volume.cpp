@@ -217,7 +217,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
         late = make_status(kUnsupported, "SGD: learning rate outside the f32 range");
         break;
       }
-      WH_HIP(launch_sgd(c.W.dtype, c.W.body, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1, s));
+      WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1, s));
     }
   }
   int stop = 0;
