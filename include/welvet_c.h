@@ -175,7 +175,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *     4, 8, 16 (at most 16 / chunks per lane; FP8, Int8, 4-bit, 8-bit table
  *     and half formats) [0]
  *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
- *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2, else 0) [-1] */
+ *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2, else 0) [-1]
+ *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
+ *     FP8 E4M3 and Int8 weights at batch > 4 [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

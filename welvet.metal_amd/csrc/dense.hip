@@ -736,6 +736,11 @@ struct GemmArgs {
   int per_block, maxspan;
   float *ws;          // [blocks][maxspan][bm][bn] partial tiles
   int bm, bn;         // tile shape
+  // split-x GEMM: xs[3][Mp][Kp] bf16 parts of A (zero past M, K); the
+  // reduction multiplies sums by post (a per-tensor scale factored out)
+  const uint16_t *xs = nullptr;
+  int Mp = 0, Kp = 0;
+  float post = 1.0f;
 };
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -980,6 +985,174 @@ __global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs a) {
   }
 }
 
+// ------------------------------------------------------ split-x bf16 GEMM
+// For formats whose decoded weights are exact in bf16 once the per-tensor
+// scale is factored out (FP8 E4M3 from the decode-ready copy, Int8 codes),
+// the fp32 product runs on the bf16 MFMA: each x is split exactly into three
+// bf16 parts (8 + 8 + 8 significand bits, by truncation: x = hi + mid + lo
+// with no rounding), so every product w * x_part is exact and the MFMA
+// accumulates in fp32 — an fp32 GEMM whose products are formed exactly, at
+// three bf16 MFMAs per fp32 one (bf16 dense rate is 16x the fp32 rate).
+//
+// C[m][n] = sum_k x[m][k] W[n][k]: MFMA 32x32x16 bf16 with A = x parts from
+// LDS and B = W decoded into registers.  Block = 4 waves x 2 column tiles of
+// 32 = 256 output columns, 32*MT batch rows; 64-deep k stages; lane (i, h)
+// of a wave reads 32 consecutive weights k0 + 32h .. + 31 of its row, and
+// MFMA step t uses bytes 8t .. 8t + 7 of them (k = k0 + 32h + 8t + j), so x
+// parts are read from LDS in the same permuted order.  Stream-K over (tile,
+// stage) like gemm_reg_kernel; partial tiles are added by sk_reduce_kernel.
+constexpr int kBf3BN = 256;
+constexpr int kBf3Row = kBK + 8;  // bf16 per LDS row: 144 B keeps 16-lane reads conflict-free
+
+// xs[p][m][k] (m < Mp, k < Kp): bf16 parts of x, zero past M and K.  A
+// non-finite x keeps its value in the high part and zero in the others.
+__global__ void __launch_bounds__(256) split_x_kernel(const float *__restrict__ x, int M, int K,
+                                                      int Mp, int Kp, uint16_t *__restrict__ xs) {
+  const int64_t total = (int64_t)Mp * Kp;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int m = (int)(i / Kp), k = (int)(i % Kp);
+    const float v = (m < M && k < K) ? x[(int64_t)m * K + k] : 0.0f;
+    const uint32_t hi = f2u(v) & 0xffff0000u;
+    const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+    const uint32_t mid = f2u(r) & 0xffff0000u;
+    const float lo = r - u2f(mid);
+    xs[i] = (uint16_t)(hi >> 16);
+    xs[total + i] = (uint16_t)(mid >> 16);
+    xs[2 * total + i] = (uint16_t)(f2u(lo) >> 16);
+  }
+}
+
+typedef short shortx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Formats the split-x GEMM takes.
+constexpr bool bf3_fmt(int f) { return f == FE4 || f == FI8; }
+
+// 8 consecutive weights (two words) as the MFMA B operand.
+template <int F>
+__device__ inline bf16x8 bf3_weights(uint32_t w0, uint32_t w1) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  bf2 p[4];
+  if constexpr (F == FE4) {
+    p[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+    p[1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+    p[2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+    p[3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  } else {  // FI8: the int8 codes (exact in bf16); the scale is applied by the reduction
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t w = q < 2 ? w0 : w1;
+      const int sh = (q & 1) * 16;
+      const float a = (float)(int8_t)(uint8_t)(w >> sh), b = (float)(int8_t)(uint8_t)(w >> (sh + 8));
+      p[q] = __builtin_bit_cast(bf2, __builtin_amdgcn_perm(f2u(b), f2u(a), 0x07060302u));
+    }
+  }
+  bf16x8 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    r[2 * q] = p[q][0];
+    r[2 * q + 1] = p[q][1];
+  }
+  return r;
+}
+
+template <int F, int MT>
+__global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
+  constexpr int BM = 32 * MT, NC = 2;
+  constexpr int XQ = 3 * BM * (kBK / 8);  // 16-byte pieces of one stage's x parts
+  constexpr int XPT = XQ / 256;           // per thread
+  static_assert(XQ % 256 == 0, "x-part pieces must divide among the threads");
+  __shared__ uint16_t Xs[2][3][BM][kBf3Row];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int T = a.gx * a.gy * a.nst;
+  int it = blockIdx.x * a.per_block;
+  const int it_end = min(T, it + a.per_block);
+  const int first_tile = it / a.nst;
+  const int64_t pstride = (int64_t)a.Mp * a.Kp;
+  // piece e = tid + 256 q of a stage: part e / (BM * 8), row (e / 8) % BM, 16-byte column e % 8
+  const int kc = tid & 7;
+  uint32_t wr[NC][8];
+  uint32_t xr[XPT][4];
+  auto load_stage = [&](int m0, int n0, int k0) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int row = min(n0 + wave * 64 + c * 32 + j, a.N - 1);
+      const uint8_t *src = a.body + (int64_t)row * a.row_bytes + k0 + 32 * h;
+      const uint4 v0 = *(const uint4 *)src, v1 = *(const uint4 *)(src + 16);
+      wr[c][0] = v0.x; wr[c][1] = v0.y; wr[c][2] = v0.z; wr[c][3] = v0.w;
+      wr[c][4] = v1.x; wr[c][5] = v1.y; wr[c][6] = v1.z; wr[c][7] = v1.w;
+    }
+#pragma unroll
+    for (int q = 0; q < XPT; ++q) {
+      const int e = tid + q * 256, m = (e >> 3) % BM, p = e / (BM * 8);
+      const uint4 v = *(const uint4 *)(a.xs + p * pstride + (int64_t)(m0 + m) * a.Kp + k0 + 8 * kc);
+      xr[q][0] = v.x; xr[q][1] = v.y; xr[q][2] = v.z; xr[q][3] = v.w;
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < XPT; ++q) {
+      const int e = tid + q * 256, m = (e >> 3) % BM, p = e / (BM * 8);
+      *(uint4 *)&Xs[buf][p][m][8 * kc] = make_uint4(xr[q][0], xr[q][1], xr[q][2], xr[q][3]);
+    }
+  };
+  while (it < it_end) {
+    const int t = it / a.nst, s0 = it % a.nst;
+    const int nseg = min(it_end, (t + 1) * a.nst) - it;
+    const int m0 = (t / a.gx) * BM, n0 = (t % a.gx) * kBf3BN;
+    floatx16 acc[MT][NC];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mt][c][i] = 0.0f;
+    load_stage(m0, n0, s0 * kBK);
+    store_x(0);
+    __syncthreads();
+    for (int s = 0; s < nseg; ++s) {
+      const int cur = s & 1;
+      bf16x8 bv[NC][4];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const bool live = n0 + wave * 64 + c * 32 + j < a.N;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bv[c][q] = bf3_weights<F>(live ? wr[c][2 * q] : 0u, live ? wr[c][2 * q + 1] : 0u);
+      }
+      if (s + 1 < nseg) load_stage(m0, n0, (s0 + s + 1) * kBK);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[cur][p][mt * 32 + j][32 * h + 8 * q]);
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+              acc[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[c][q], acc[mt][c], 0, 0, 0);
+          }
+        }
+      }
+      if (s + 1 < nseg) store_x(cur ^ 1);
+      __syncthreads();
+    }
+    // D[m][n]: lane (j, h) holds column j, rows 8*(r/4) + 4*h + r%4
+    float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * kBf3BN);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          dst[m * kBf3BN + wave * 64 + c * 32 + j] = acc[mt][c][r];
+        }
+    it += nseg;
+  }
+}
+
 // Sum of a tile's stream-K partials in workgroup order (f64).  Grid: x =
 // tile, y = 1024-element slice of the tile; each thread adds four adjacent
 // outputs with float4 loads.  The forward applies bias + activation, dX
@@ -1021,6 +1194,7 @@ __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double
   for (int i = 0; i < 4; ++i) {
     if (n + i >= a.N) break;
     const int64_t idx = (int64_t)m * a.N + n + i;
+    if (a.post != 1.0f) sum[i] *= (double)a.post;
     if constexpr (FWD) bias_act_store(sum[i], n + i, bias, bias_len, act, out, post, idx);
     else out[idx] = (float)sum[i];
   }
@@ -1193,7 +1367,7 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1};
 
 inline int blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
@@ -1252,7 +1426,10 @@ int num_cus() {
 
 struct SkPlan {
   int gx, gy, nst, per_block, blocks, maxspan, bm, bn;
-  size_t ws_bytes;
+  size_t ws_bytes;  // whole workspace: partial tiles (+ x parts of the split-x GEMM)
+  // split-x GEMM: x parts xs[3][Mp][Kp] at byte offset xs_off of the workspace
+  int Mp = 0, Kp = 0;
+  size_t xs_off = 0;
 };
 
 // Stream-K split of an M x N x K product over bm x bn tiles into equal
@@ -1279,9 +1456,20 @@ dim3 sk_reduce_grid(const SkPlan &p) {
 
 bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // formats of <= 16 bits
 
-// Forward GEMM plan: the register-B kernel for <= 16-bit formats, else the
-// LDS-staged kernel.
+bool use_bf3(int f) { return bf3_fmt(f) && g_tune[kTuneBf3] != 0; }
+
+// Forward GEMM plan: the split-x bf16 kernel for the formats it takes, the
+// register-B kernel for other <= 16-bit formats, else the LDS-staged kernel.
 SkPlan plan_fwd_gemm(int f, int M, int K, int N) {
+  if (use_bf3(f)) {
+    const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
+    SkPlan p = plan_sk(M, K, N, M <= 32 ? 32 : 64, kBf3BN, occ);
+    p.Mp = (M + p.bm - 1) / p.bm * p.bm;
+    p.Kp = p.nst * kBK;
+    p.xs_off = (p.ws_bytes + 255) / 256 * 256;
+    p.ws_bytes = p.xs_off + (size_t)3 * p.Mp * p.Kp * sizeof(uint16_t);
+    return p;
+  }
   if (reg_gemm_ok(f) && g_tune[kTuneRegGemm] != 0) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
     return plan_sk(M, K, N, M <= 32 ? 32 : 64, kRegBN, occ);
@@ -1463,7 +1651,22 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
   GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
              p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
-  if (p.bn == kRegBN) {
+  if (p.bn == kBf3BN) {
+    uint16_t *xs = (uint16_t *)((char *)ws + p.xs_off);
+    a.xs = xs;
+    a.Mp = p.Mp;
+    a.Kp = p.Kp;
+    a.post = f == FI8 ? w.scale : 1.0f;
+    split_x_kernel<<<blocks_for((int64_t)p.Mp * p.Kp), 256, 0, s>>>(x, batch, w.cols, p.Mp, p.Kp, xs);
+#define WH_GB(F)                                                                      \
+  if constexpr (bf3_fmt(F)) {                                                         \
+    if (p.bm == 32) gemm_bf3_kernel<F, 1><<<p.blocks, 256, 0, s>>>(a);                \
+    else gemm_bf3_kernel<F, 2><<<p.blocks, 256, 0, s>>>(a);                           \
+  }                                                                                   \
+  break;
+    WH_FMT_SWITCH(f, WH_GB)
+#undef WH_GB
+  } else if (p.bn == kRegBN) {
 #define WH_GR(F)                                                                      \
   if constexpr (FI<F>::kBits <= 16) {                                                 \
     if (p.bm == 32) gemm_reg_kernel<F, 1><<<p.blocks, 256, 0, s>>>(a);                \

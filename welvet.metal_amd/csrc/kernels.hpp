@@ -79,10 +79,11 @@ void set_forward_path(int path);
 // 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
 // 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
 // block per row group; -1 = auto: 16 for the FP8 converter formats, else 0).
+// 10 split-x bf16 MFMA GEMM for FP8 E4M3 and Int8 (1 on).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
-  kNumTune = 10
+  kTuneBf3 = 10, kNumTune = 11
 };
 int set_tuning(int key, int value);
 
