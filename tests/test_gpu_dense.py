@@ -73,7 +73,9 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(gemv_rows=16, cr=3), dict(gemv_rows=8, cr=1), dict(gemv_rows=16, cr=3, pair_lut=0),
          dict(gemv_waves=0), dict(gemv_waves=1), dict(gemv_waves=12), dict(gemv_waves=1, cr=1),
          dict(gemv_waves=2, gemv_rows=16, cr=3), dict(gemv_waves=1, gemv_rows=1, pair_lut=0),
-         dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4)]
+         dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4), dict(bf3_depth=2),
+         dict(bf3_depth=3), dict(bf3_depth=3, gemm_occ=1), dict(bf3_cols=1),
+         dict(bf3_cols=1, gemm_occ=1)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])

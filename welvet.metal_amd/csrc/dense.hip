@@ -736,10 +736,8 @@ struct GemmArgs {
   int per_block, maxspan;
   float *ws;          // [blocks][maxspan][bm][bn] partial tiles
   int bm, bn;         // tile shape
-  // split-x GEMM: xs[3][Mp][Kp] bf16 parts of A (zero past M, K); the
-  // reduction multiplies sums by post (a per-tensor scale factored out)
-  const uint16_t *xs = nullptr;
-  int Mp = 0, Kp = 0;
+  // the reduction multiplies sums by post (a per-tensor scale the split-x
+  // GEMM factors out of the weights)
   float post = 1.0f;
 };
 
@@ -995,32 +993,13 @@ __global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs a) {
 // three bf16 MFMAs per fp32 one (bf16 dense rate is 16x the fp32 rate).
 //
 // C[m][n] = sum_k x[m][k] W[n][k]: MFMA 32x32x16 bf16 with A = x parts from
-// LDS and B = W decoded into registers.  Block = 4 waves x 2 column tiles of
-// 32 = 256 output columns, 32*MT batch rows; 64-deep k stages; lane (i, h)
+// LDS and B = W decoded into registers.  Block = 4 waves x NC column tiles
+// of 32 = 128*NC output columns, 32*MT batch rows; 64-deep k stages; lane (i, h)
 // of a wave reads 32 consecutive weights k0 + 32h .. + 31 of its row, and
 // MFMA step t uses bytes 8t .. 8t + 7 of them (k = k0 + 32h + 8t + j), so x
 // parts are read from LDS in the same permuted order.  Stream-K over (tile,
 // stage) like gemm_reg_kernel; partial tiles are added by sk_reduce_kernel.
-constexpr int kBf3BN = 256;
 constexpr int kBf3Row = kBK + 8;  // bf16 per LDS row: 144 B keeps 16-lane reads conflict-free
-
-// xs[p][m][k] (m < Mp, k < Kp): bf16 parts of x, zero past M and K.  A
-// non-finite x keeps its value in the high part and zero in the others.
-__global__ void __launch_bounds__(256) split_x_kernel(const float *__restrict__ x, int M, int K,
-                                                      int Mp, int Kp, uint16_t *__restrict__ xs) {
-  const int64_t total = (int64_t)Mp * Kp;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int m = (int)(i / Kp), k = (int)(i % Kp);
-    const float v = (m < M && k < K) ? x[(int64_t)m * K + k] : 0.0f;
-    const uint32_t hi = f2u(v) & 0xffff0000u;
-    const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
-    const uint32_t mid = f2u(r) & 0xffff0000u;
-    const float lo = r - u2f(mid);
-    xs[i] = (uint16_t)(hi >> 16);
-    xs[total + i] = (uint16_t)(mid >> 16);
-    xs[2 * total + i] = (uint16_t)(f2u(lo) >> 16);
-  }
-}
 
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -1056,12 +1035,11 @@ __device__ inline bf16x8 bf3_weights(uint32_t w0, uint32_t w1) {
   return r;
 }
 
-template <int F, int MT>
+template <int F, int MT, int D, int NC>
 __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
-  constexpr int BM = 32 * MT, NC = 2;
-  constexpr int XQ = 3 * BM * (kBK / 8);  // 16-byte pieces of one stage's x parts
-  constexpr int XPT = XQ / 256;           // per thread
-  static_assert(XQ % 256 == 0, "x-part pieces must divide among the threads");
+  constexpr int BM = 32 * MT, BN = 128 * NC;
+  constexpr int XE = BM * kBK / 256;  // x values per thread per stage (8 or 16)
+  constexpr int XT = kBK / XE;        // threads per x row
   __shared__ uint16_t Xs[2][3][BM][kBf3Row];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
@@ -1069,87 +1047,140 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
   int it = blockIdx.x * a.per_block;
   const int it_end = min(T, it + a.per_block);
   const int first_tile = it / a.nst;
-  const int64_t pstride = (int64_t)a.Mp * a.Kp;
-  // piece e = tid + 256 q of a stage: part e / (BM * 8), row (e / 8) % BM, 16-byte column e % 8
-  const int kc = tid & 7;
-  uint32_t wr[NC][8];
-  uint32_t xr[XPT][4];
-  auto load_stage = [&](int m0, int n0, int k0) {
+  // thread's x piece of a stage: row xm, k offset xk .. xk + XE - 1 (K is a
+  // multiple of 16, so a piece lies wholly inside or outside the row)
+  const int xm = tid / XT, xk = (tid % XT) * XE;
+  uint32_t wr[D][NC][8];  // weights of units u .. u + D - 1 (ring slot = unit offset mod D)
+  float xf[D][XE];         // x of the same units
+  // unit u of the block's share = (tile u / nst, stage u % nst)
+  auto unit_m0 = [&](int u) { return (u / a.nst / a.gx) * BM; };
+  auto unit_n0 = [&](int u) { return (u / a.nst % a.gx) * BN; };
+  auto load_w = [&](int u, uint32_t (&w)[NC][8]) {
+    const int n0 = unit_n0(u), k0 = (u % a.nst) * kBK;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int row = min(n0 + wave * 64 + c * 32 + j, a.N - 1);
+      const int row = min(n0 + wave * 32 * NC + c * 32 + j, a.N - 1);
       const uint8_t *src = a.body + (int64_t)row * a.row_bytes + k0 + 32 * h;
       const uint4 v0 = *(const uint4 *)src, v1 = *(const uint4 *)(src + 16);
-      wr[c][0] = v0.x; wr[c][1] = v0.y; wr[c][2] = v0.z; wr[c][3] = v0.w;
-      wr[c][4] = v1.x; wr[c][5] = v1.y; wr[c][6] = v1.z; wr[c][7] = v1.w;
-    }
-#pragma unroll
-    for (int q = 0; q < XPT; ++q) {
-      const int e = tid + q * 256, m = (e >> 3) % BM, p = e / (BM * 8);
-      const uint4 v = *(const uint4 *)(a.xs + p * pstride + (int64_t)(m0 + m) * a.Kp + k0 + 8 * kc);
-      xr[q][0] = v.x; xr[q][1] = v.y; xr[q][2] = v.z; xr[q][3] = v.w;
+      w[c][0] = v0.x; w[c][1] = v0.y; w[c][2] = v0.z; w[c][3] = v0.w;
+      w[c][4] = v1.x; w[c][5] = v1.y; w[c][6] = v1.z; w[c][7] = v1.w;
     }
   };
-  auto store_x = [&](int buf) {
+  // raw loads: a value is masked where it is stored, so the load's latency
+  // is not exposed here
+  uint32_t xin[D];         // ~0 when the slot's x piece lies inside x, else 0
+  auto load_x = [&](int u, float (&xf)[XE], uint32_t &in_mask) {
+    const int m0 = unit_m0(u), k0 = (u % a.nst) * kBK;
+    const bool in = m0 + xm < a.M && k0 + xk < a.K;
+    in_mask = in ? ~0u : 0u;
+    const float *src = a.A + (int64_t)(in ? m0 + xm : 0) * a.K + (in ? k0 + xk : 0);
 #pragma unroll
-    for (int q = 0; q < XPT; ++q) {
-      const int e = tid + q * 256, m = (e >> 3) % BM, p = e / (BM * 8);
-      *(uint4 *)&Xs[buf][p][m][8 * kc] = make_uint4(xr[q][0], xr[q][1], xr[q][2], xr[q][3]);
+    for (int i = 0; i < XE; i += 4) {
+      const float4 v = *(const float4 *)(src + i);
+      xf[i] = v.x;
+      xf[i + 1] = v.y;
+      xf[i + 2] = v.z;
+      xf[i + 3] = v.w;
     }
   };
-  while (it < it_end) {
-    const int t = it / a.nst, s0 = it % a.nst;
-    const int nseg = min(it_end, (t + 1) * a.nst) - it;
-    const int m0 = (t / a.gx) * BM, n0 = (t % a.gx) * kBf3BN;
-    floatx16 acc[MT][NC];
+  // x = hi + mid + lo exactly: truncations to the top 8 significand bits,
+  // remainders exact in f32 (a non-finite x keeps its value in hi)
+  auto store_x = [&](int buf, const float (&xf)[XE], uint32_t in_mask) {
+    uint32_t wp[3][XE / 2];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int i = 0; i < XE; i += 2) {
+      uint32_t part[3][2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = u2f(f2u(xf[i + e]) & in_mask);
+        const uint32_t hi = f2u(v) & 0xffff0000u;
+        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const uint32_t mid = f2u(r) & 0xffff0000u;
+        part[0][e] = hi;
+        part[1][e] = mid;
+        part[2][e] = f2u(r - u2f(mid));
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) wp[p][i / 2] = __builtin_amdgcn_perm(part[p][1], part[p][0], 0x07060302u);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int q = 0; q < XE / 8; ++q)
+        *(uint4 *)&Xs[buf][p][xm][xk + 8 * q] =
+            make_uint4(wp[p][4 * q], wp[p][4 * q + 1], wp[p][4 * q + 2], wp[p][4 * q + 3]);
+  };
+  // The block's units run as one stream across tile boundaries: unit u
+  // takes ring slot (u - it) mod D, whose weights and x were loaded D units
+  // earlier; the slot is refilled with unit u + D once unit u's weights are
+  // decoded (its x went to LDS one unit earlier).  A tile's partial sum is
+  // written after its last unit here.  Rows past N read row N - 1 (finite
+  // codes) and their columns are never stored.
+  floatx16 acc[MT][NC];
+  int buf = 0;
+  // loads past the share re-read its last unit (valid addresses, unused
+  // data): unconditional loads keep the wait counts static
+  const int last = max(it, it_end - 1);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load_w(min(it + d, last), wr[d]);
+    load_x(min(it + d, last), xf[d], xin[d]);
+  }
+  store_x(0, xf[0], xin[0]);
+  __syncthreads();
+  for (int u0 = it; u0 < it_end; u0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int u = u0 + d;
+      if (u >= it_end) break;
+      const int t = u / a.nst, st = u - t * a.nst;
+      if (u == it || st == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mt][c][i] = 0.0f;
+      }
+      bf16x8 bv[NC][4];
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[mt][c][i] = 0.0f;
-    load_stage(m0, n0, s0 * kBK);
-    store_x(0);
-    __syncthreads();
-    for (int s = 0; s < nseg; ++s) {
-      const int cur = s & 1;
-      bf16x8 bv[NC][4];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const bool live = n0 + wave * 64 + c * 32 + j < a.N;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          bv[c][q] = bf3_weights<F>(live ? wr[c][2 * q] : 0u, live ? wr[c][2 * q + 1] : 0u);
-      }
-      if (s + 1 < nseg) load_stage(m0, n0, (s0 + s + 1) * kBK);
+        for (int q = 0; q < 4; ++q) bv[c][q] = bf3_weights<F>(wr[d][c][2 * q], wr[d][c][2 * q + 1]);
+      load_w(min(u + D, last), wr[d]);
+      load_x(min(u + D, last), xf[d], xin[d]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int p = 0; p < 3; ++p) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[cur][p][mt * 32 + j][32 * h + 8 * q]);
+            const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[buf][p][mt * 32 + j][32 * h + 8 * q]);
 #pragma unroll
             for (int c = 0; c < NC; ++c)
               acc[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[c][q], acc[mt][c], 0, 0, 0);
           }
         }
       }
-      if (s + 1 < nseg) store_x(cur ^ 1);
+      store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
       __syncthreads();
+      buf ^= 1;
+      if (st == a.nst - 1 || u + 1 == it_end) {
+        // D[m][n]: lane (j, h) holds column j, rows 8*(r/4) + 4*h + r%4
+        // rows past M are never read by the reduction: not stored
+        float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * BN);
+        const int mrows = a.M - unit_m0(u);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+              if (m < mrows) dst[m * BN + wave * 32 * NC + c * 32 + j] = acc[mt][c][r];
+            }
+      }
     }
-    // D[m][n]: lane (j, h) holds column j, rows 8*(r/4) + 4*h + r%4
-    float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * kBf3BN);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          dst[m * kBf3BN + wave * 64 + c * 32 + j] = acc[mt][c][r];
-        }
-    it += nseg;
   }
 }
 
@@ -1367,7 +1398,7 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0};
 
 inline int blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
@@ -1426,10 +1457,8 @@ int num_cus() {
 
 struct SkPlan {
   int gx, gy, nst, per_block, blocks, maxspan, bm, bn;
-  size_t ws_bytes;  // whole workspace: partial tiles (+ x parts of the split-x GEMM)
-  // split-x GEMM: x parts xs[3][Mp][Kp] at byte offset xs_off of the workspace
-  int Mp = 0, Kp = 0;
-  size_t xs_off = 0;
+  size_t ws_bytes;
+  bool bf3 = false;  // split-x GEMM plan (bn = 128 or 256)
 };
 
 // Stream-K split of an M x N x K product over bm x bn tiles into equal
@@ -1463,11 +1492,9 @@ bool use_bf3(int f) { return bf3_fmt(f) && g_tune[kTuneBf3] != 0; }
 SkPlan plan_fwd_gemm(int f, int M, int K, int N) {
   if (use_bf3(f)) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
-    SkPlan p = plan_sk(M, K, N, M <= 32 ? 32 : 64, kBf3BN, occ);
-    p.Mp = (M + p.bm - 1) / p.bm * p.bm;
-    p.Kp = p.nst * kBK;
-    p.xs_off = (p.ws_bytes + 255) / 256 * 256;
-    p.ws_bytes = p.xs_off + (size_t)3 * p.Mp * p.Kp * sizeof(uint16_t);
+    const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
+    SkPlan p = plan_sk(M, K, N, M <= 32 ? 32 : 64, bn, occ);
+    p.bf3 = true;
     return p;
   }
   if (reg_gemm_ok(f) && g_tune[kTuneRegGemm] != 0) {
@@ -1651,17 +1678,21 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
   GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
              p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
-  if (p.bn == kBf3BN) {
-    uint16_t *xs = (uint16_t *)((char *)ws + p.xs_off);
-    a.xs = xs;
-    a.Mp = p.Mp;
-    a.Kp = p.Kp;
+  if (p.bf3) {
     a.post = f == FI8 ? w.scale : 1.0f;
-    split_x_kernel<<<blocks_for((int64_t)p.Mp * p.Kp), 256, 0, s>>>(x, batch, w.cols, p.Mp, p.Kp, xs);
+    const int dep = g_tune[kTuneBf3Depth];
 #define WH_GB(F)                                                                      \
   if constexpr (bf3_fmt(F)) {                                                         \
-    if (p.bm == 32) gemm_bf3_kernel<F, 1><<<p.blocks, 256, 0, s>>>(a);                \
-    else gemm_bf3_kernel<F, 2><<<p.blocks, 256, 0, s>>>(a);                           \
+    if (p.bm == 32) {                                                                 \
+      if (p.bn == 128) gemm_bf3_kernel<F, 1, 1, 1><<<p.blocks, 256, 0, s>>>(a);        \
+      else if (dep == 2) gemm_bf3_kernel<F, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a);      \
+      else if (dep == 3) gemm_bf3_kernel<F, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);      \
+      else gemm_bf3_kernel<F, 1, 1, 2><<<p.blocks, 256, 0, s>>>(a);                    \
+    } else {                                                                          \
+      if (p.bn == 128) gemm_bf3_kernel<F, 2, 1, 1><<<p.blocks, 256, 0, s>>>(a);        \
+      else if (dep == 2) gemm_bf3_kernel<F, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a);      \
+      else gemm_bf3_kernel<F, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                    \
+    }                                                                                 \
   }                                                                                   \
   break;
     WH_FMT_SWITCH(f, WH_GB)

@@ -79,11 +79,13 @@ void set_forward_path(int path);
 // 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
 // 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
 // block per row group; -1 = auto: 16 for the FP8 converter formats, else 0).
-// 10 split-x bf16 MFMA GEMM for FP8 E4M3 and Int8 (1 on).
+// 10 split-x bf16 MFMA GEMM for FP8 E4M3 and Int8 (1 on), 11 its weight
+// prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
+// width (0: 256 output columns, 1: 128).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
-  kTuneBf3 = 10, kNumTune = 11
+  kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kNumTune = 13
 };
 int set_tuning(int key, int value);
 
