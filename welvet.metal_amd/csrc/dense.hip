@@ -1167,7 +1167,8 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
       buf ^= 1;
       if (st == a.nst - 1 || u + 1 == it_end) {
         // D[m][n]: lane (j, h) holds column j, rows 8*(r/4) + 4*h + r%4
-        // rows past M are never read by the reduction: not stored
+        // groups of 8 rows wholly past M are never read by the reduction:
+        // not stored (a wave-uniform test)
         float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * BN);
         const int mrows = a.M - unit_m0(u);
 #pragma unroll
@@ -1177,7 +1178,7 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-              if (m < mrows) dst[m * BN + wave * 32 * NC + c * 32 + j] = acc[mt][c][r];
+              if (mt * 32 + 8 * (r >> 2) < mrows) dst[m * BN + wave * 32 * NC + c * 32 + j] = acc[mt][c][r];
             }
       }
     }
