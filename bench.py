@@ -39,7 +39,7 @@ METRIC = "Dense fwd HBM GB/s (batch 1) & TFLOP/s (batch 64), FP8/NF4 4096x11008"
 HBM_PEAK = 8000.0        # GB/s, MI355X
 FP32_MFMA_PEAK = 157.3   # TFLOP/s, MI355X dense fp32 matrix
 BF16_MFMA_PEAK = 2500.0  # TFLOP/s, MI355X dense bf16 matrix
-SPLIT_X_DTYPES = ("fp8e4m3", "int8")  # weights the split-x bf16 GEMM takes
+SPLIT_X_DTYPES = ("fp8e4m3", "int8", "fp4", "nf4")  # weights the split-x bf16 GEMM takes
 IN, OUT = 4096, 11008
 MALL_BYTES = 512 << 20   # rotate past 2x the 256 MB Infinity Cache
 
@@ -351,10 +351,11 @@ def main():
         r["roofline_frac"] = (r["hbm_gbs"] / HBM_PEAK if r["batch"] == 1
                               else r["tflops"] / FP32_MFMA_PEAK)
         if r["batch"] > 4 and r["weight_dtype"] in SPLIT_X_DTYPES:
-            # the split-x GEMM runs the fp32 product as three exact bf16 MFMA
-            # products: executed bf16 flops = 3x algorithmic, against the bf16 peak
+            # the split-x GEMM runs the fp32 product as exact bf16 MFMA
+            # products: 3 per product (6 for NF4, whose table values are split
+            # too); executed bf16 flops against the bf16 peak
             r["gemm"] = "split-x bf16 MFMA (x = hi + mid + lo exactly; fp32 accumulate)"
-            r["bf16_mfma_frac"] = 3 * r["tflops"] / BF16_MFMA_PEAK
+            r["bf16_mfma_frac"] = (6 if r["weight_dtype"] == "nf4" else 3) * r["tflops"] / BF16_MFMA_PEAK
             r["hbm_frac"] = r["hbm_gbs"] / HBM_PEAK
         elif r["batch"] > 4:
             r["gemm"] = "fp32 MFMA (v_mfma_f32_32x32x2f32)"

@@ -177,7 +177,7 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
  *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2, else 0) [-1]
  *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
- *     FP8 E4M3 and Int8 weights at batch > 4 [1]
+ *     FP8 E4M3, Int8, FP4 and NF4 weights at batch > 4 [1]
  *   11 its weight prefetch depth in k stages: 1, 2, or 3 (batch <= 32) [1]
  *   12 its block width: 0 = 256 output columns, 1 = 128 [0] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);

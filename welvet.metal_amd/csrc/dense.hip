@@ -1004,45 +1004,98 @@ constexpr int kBf3Row = kBK + 8;  // bf16 per LDS row: 144 B keeps 16-lane reads
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// Formats the split-x GEMM takes.
-constexpr bool bf3_fmt(int f) { return f == FE4 || f == FI8; }
+// Weight kinds the split-x GEMM takes.  Every decoded weight is exact in
+// bf16 once the per-tensor scale (applied by the reduction) is factored out:
+// E4M3 from the decode-ready copy, Int8 and FP4 codes as they are, and NF4
+// table values as three exact bf16 parts (hi + mid + lo, like x).
+enum Bf3Kind { BK_E4 = 0, BK_I8 = 1, BK_FP4 = 2, BK_NF4 = 3 };
 
-// 8 consecutive weights (two words) as the MFMA B operand.
-template <int F>
-__device__ inline bf16x8 bf3_weights(uint32_t w0, uint32_t w1) {
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  bf2 p[4];
-  if constexpr (F == FE4) {
-    p[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
-    p[1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
-    p[2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
-    p[3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
-  } else {  // FI8: the int8 codes (exact in bf16); the scale is applied by the reduction
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t w = q < 2 ? w0 : w1;
-      const int sh = (q & 1) * 16;
-      const float a = (float)(int8_t)(uint8_t)(w >> sh), b = (float)(int8_t)(uint8_t)(w >> (sh + 8));
-      p[q] = __builtin_bit_cast(bf2, __builtin_amdgcn_perm(f2u(b), f2u(a), 0x07060302u));
-    }
-  }
+template <int BK>
+struct B3 {
+  static constexpr int kBits = BK <= BK_I8 ? 8 : 4;
+  static constexpr int kWords = kBits;  // words of a lane's 32 weights per stage
+  static constexpr int kParts = BK == BK_NF4 ? 3 : 1;
+};
+
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+inline __device__ bf16x8 bf16x8_of(const uint32_t (&u)[4]) {
   bf16x8 r;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    r[2 * q] = p[q][0];
-    r[2 * q + 1] = p[q][1];
+    const bf16x2v p = __builtin_bit_cast(bf16x2v, u[q]);
+    r[2 * q] = p[0];
+    r[2 * q + 1] = p[1];
   }
   return r;
 }
 
-template <int F, int MT, int D, int NC>
+// 8 consecutive weights (the words of MFMA step q) as B operands: parts[0..P).
+// NF4 reads the split table t3[code] = {hi | mid << 16, lo}.
+template <int BK>
+__device__ inline void bf3_weights(const uint32_t *w, int q, const uint2 *t3, bf16x8 (&parts)[B3<BK>::kParts]) {
+  if constexpr (BK == BK_E4) {
+    const uint32_t w0 = w[2 * q], w1 = w[2 * q + 1];
+    const uint32_t u[4] = {
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+    parts[0] = bf16x8_of(u);
+  } else if constexpr (BK == BK_I8) {
+    uint32_t u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wd = w[2 * q + (i >> 1)];
+      const int sh = (i & 1) * 16;
+      const float lo = (float)(int8_t)(uint8_t)(wd >> sh), hi = (float)(int8_t)(uint8_t)(wd >> (sh + 8));
+      u[i] = __builtin_amdgcn_perm(f2u(hi), f2u(lo), 0x07060302u);
+    }
+    parts[0] = bf16x8_of(u);
+  } else if constexpr (BK == BK_FP4) {
+    const uint32_t wd = w[q];
+    const uint32_t u[4] = {
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, 1.0f, 0)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, 1.0f, 1)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, 1.0f, 2)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, 1.0f, 3))};
+    parts[0] = bf16x8_of(u);
+  } else {  // NF4
+    const uint32_t wd = w[q];
+    uint32_t hi[4], mid[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint2 e0 = t3[(wd >> (8 * i)) & 15u], e1 = t3[(wd >> (8 * i + 4)) & 15u];
+      hi[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x05040100u);
+      mid[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x07060302u);
+      lo[i] = __builtin_amdgcn_perm(e1.y, e0.y, 0x05040100u);
+    }
+    parts[0] = bf16x8_of(hi);
+    parts[1] = bf16x8_of(mid);
+    parts[2] = bf16x8_of(lo);
+  }
+}
+
+template <int BK, int MT, int D, int NC>
 __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
-  constexpr int BM = 32 * MT, BN = 128 * NC;
+  using K3 = B3<BK>;
+  constexpr int BM = 32 * MT, BN = 128 * NC, NW = K3::kWords, NP = K3::kParts;
   constexpr int XE = BM * kBK / 256;  // x values per thread per stage (8 or 16)
   constexpr int XT = kBK / XE;        // threads per x row
   __shared__ uint16_t Xs[2][3][BM][kBf3Row];
+  __shared__ uint2 t3[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
+  if constexpr (BK == BK_NF4) {
+    if (tid < 16) {  // NF4 table values split exactly into three bf16 parts
+      const float t = kNf4Tab[tid];
+      const uint32_t hi = f2u(t) & 0xffff0000u;
+      const float r = t - u2f(hi);
+      const uint32_t mid = f2u(r) & 0xffff0000u;
+      const uint32_t lo = f2u(r - u2f(mid));
+      t3[tid] = make_uint2((hi >> 16) | mid, lo >> 16);
+    }
+  }
   const int T = a.gx * a.gy * a.nst;
   int it = blockIdx.x * a.per_block;
   const int it_end = min(T, it + a.per_block);
@@ -1050,20 +1103,22 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
   // thread's x piece of a stage: row xm, k offset xk .. xk + XE - 1 (K is a
   // multiple of 16, so a piece lies wholly inside or outside the row)
   const int xm = tid / XT, xk = (tid % XT) * XE;
-  uint32_t wr[D][NC][8];  // weights of units u .. u + D - 1 (ring slot = unit offset mod D)
+  uint32_t wr[D][NC][NW];  // weights of units u .. u + D - 1 (ring slot = unit offset mod D)
   float xf[D][XE];         // x of the same units
   // unit u of the block's share = (tile u / nst, stage u % nst)
   auto unit_m0 = [&](int u) { return (u / a.nst / a.gx) * BM; };
   auto unit_n0 = [&](int u) { return (u / a.nst % a.gx) * BN; };
-  auto load_w = [&](int u, uint32_t (&w)[NC][8]) {
+  auto load_w = [&](int u, uint32_t (&w)[NC][NW]) {
     const int n0 = unit_n0(u), k0 = (u % a.nst) * kBK;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int row = min(n0 + wave * 32 * NC + c * 32 + j, a.N - 1);
-      const uint8_t *src = a.body + (int64_t)row * a.row_bytes + k0 + 32 * h;
-      const uint4 v0 = *(const uint4 *)src, v1 = *(const uint4 *)(src + 16);
-      w[c][0] = v0.x; w[c][1] = v0.y; w[c][2] = v0.z; w[c][3] = v0.w;
-      w[c][4] = v1.x; w[c][5] = v1.y; w[c][6] = v1.z; w[c][7] = v1.w;
+      const uint8_t *src = a.body + (int64_t)row * a.row_bytes + (k0 + 32 * h) * K3::kBits / 8;
+#pragma unroll
+      for (int i = 0; i < NW; i += 4) {
+        const uint4 v = *(const uint4 *)(src + 4 * i);
+        w[c][i] = v.x; w[c][i + 1] = v.y; w[c][i + 2] = v.z; w[c][i + 3] = v.w;
+      }
     }
   };
   // raw loads: a value is masked where it is stored, so the load's latency
@@ -1110,6 +1165,23 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
         *(uint4 *)&Xs[buf][p][xm][xk + 8 * q] =
             make_uint4(wp[p][4 * q], wp[p][4 * q + 1], wp[p][4 * q + 2], wp[p][4 * q + 3]);
   };
+  // One MFMA step: products of x part p with weight part wp for p + wp <= 2
+  // (the dropped NF4 terms are below 2^-23 of each product).
+  auto mfma_step = [&](floatx16 (&acc)[MT][NC], int buf, int q, const bf16x8 (&bv)[NC][NP]) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[buf][p][mt * 32 + j][32 * h + 8 * q]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int wp = 0; wp < NP; ++wp)
+            if (p + wp <= 2)
+              acc[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[c][wp], acc[mt][c], 0, 0, 0);
+      }
+    }
+  };
   // The block's units run as one stream across tile boundaries: unit u
   // takes ring slot (u - it) mod D, whose weights and x were loaded D units
   // earlier; the slot is refilled with unit u + D once unit u's weights are
@@ -1142,32 +1214,39 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][c][i] = 0.0f;
       }
-      bf16x8 bv[NC][4];
+      if constexpr (NP == 1) {
+        // decode the unit's weights, refill the slot, then the MFMAs
+        bf16x8 bv[4][NC][1];
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bv[c][q] = bf3_weights<F>(wr[d][c][2 * q], wr[d][c][2 * q + 1]);
-      load_w(min(u + D, last), wr[d]);
-      load_x(min(u + D, last), xf[d], xin[d]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int p = 0; p < 3; ++p) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[buf][p][mt * 32 + j][32 * h + 8 * q]);
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-              acc[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[c][q], acc[mt][c], 0, 0, 0);
+          for (int c = 0; c < NC; ++c) {
+            bf16x8 pp[1];
+            bf3_weights<BK>(wr[d][c], q, t3, pp);
+            bv[q][c][0] = pp[0];
           }
+        load_w(min(u + D, last), wr[d]);
+        load_x(min(u + D, last), xf[d], xin[d]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mfma_step(acc, buf, q, bv[q]);
+      } else {
+        // three weight parts: decode step by step, refill the slot afterwards
+        load_x(min(u + D, last), xf[d], xin[d]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bf16x8 bv[NC][NP];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) bf3_weights<BK>(wr[d][c], q, t3, bv[c]);
+          mfma_step(acc, buf, q, bv);
         }
+        load_w(min(u + D, last), wr[d]);
       }
       store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
       __syncthreads();
       buf ^= 1;
       if (st == a.nst - 1 || u + 1 == it_end) {
-        // D[m][n]: lane (j, h) holds column j, rows 8*(r/4) + 4*h + r%4
-        // groups of 8 rows wholly past M are never read by the reduction:
+        // D[m][n]: lane (j, h) holds column j, rows 8*(r/4) + 4*h + r%4.
+        // Groups of 8 rows wholly past M are never read by the reduction:
         // not stored (a wave-uniform test)
         float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * BN);
         const int mrows = a.M - unit_m0(u);
@@ -1401,6 +1480,17 @@ int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
 int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0};
 
+// Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
+// take it.
+int bf3_kind(int dt) {
+  if (g_tune[kTuneBf3] == 0) return -1;
+  if (dt == kFP8E4M3 && g_tune[kTuneFastDecode] != 0) return BK_E4;
+  if (dt == kInt8) return BK_I8;
+  if (dt == kFP4) return BK_FP4;
+  if (dt == kNF4) return BK_NF4;
+  return -1;
+}
+
 inline int blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
   return (int)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
@@ -1486,12 +1576,11 @@ dim3 sk_reduce_grid(const SkPlan &p) {
 
 bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // formats of <= 16 bits
 
-bool use_bf3(int f) { return bf3_fmt(f) && g_tune[kTuneBf3] != 0; }
 
 // Forward GEMM plan: the split-x bf16 kernel for the formats it takes, the
 // register-B kernel for other <= 16-bit formats, else the LDS-staged kernel.
-SkPlan plan_fwd_gemm(int f, int M, int K, int N) {
-  if (use_bf3(f)) {
+SkPlan plan_fwd_gemm(int f, int dt, int M, int K, int N) {
+  if (bf3_kind(dt) >= 0) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
     const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
     SkPlan p = plan_sk(M, K, N, M <= 32 ? 32 : 64, bn, occ);
@@ -1570,7 +1659,7 @@ int set_tuning(int key, int value) {
 
 size_t forward_workspace_bytes(const DevStore &w, int batch) {
   if (fwd_route(w, batch) != 2) return 0;
-  return plan_fwd_gemm(kernel_fmt(w.dtype), batch, w.cols, w.rows).ws_bytes;
+  return plan_fwd_gemm(kernel_fmt(w.dtype), w.dtype, batch, w.cols, w.rows).ws_bytes;
 }
 
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
@@ -1675,28 +1764,33 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
     WH_FMT_SWITCH(f, WH_GV)
 #undef WH_GV
   }
-  const SkPlan p = plan_fwd_gemm(f, batch, w.cols, w.rows);
+  const SkPlan p = plan_fwd_gemm(f, w.dtype, batch, w.cols, w.rows);
   if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
   GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
              p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
   if (p.bf3) {
-    a.post = f == FI8 ? w.scale : 1.0f;
+    const int bk = bf3_kind(w.dtype);
+    a.post = (bk == BK_I8 || bk == BK_NF4) ? w.scale : 1.0f;
+    if (bk == BK_E4) a.body = w.kbody;
     const int dep = g_tune[kTuneBf3Depth];
-#define WH_GB(F)                                                                      \
-  if constexpr (bf3_fmt(F)) {                                                         \
-    if (p.bm == 32) {                                                                 \
-      if (p.bn == 128) gemm_bf3_kernel<F, 1, 1, 1><<<p.blocks, 256, 0, s>>>(a);        \
-      else if (dep == 2) gemm_bf3_kernel<F, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a);      \
-      else if (dep == 3) gemm_bf3_kernel<F, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);      \
-      else gemm_bf3_kernel<F, 1, 1, 2><<<p.blocks, 256, 0, s>>>(a);                    \
-    } else {                                                                          \
-      if (p.bn == 128) gemm_bf3_kernel<F, 2, 1, 1><<<p.blocks, 256, 0, s>>>(a);        \
-      else if (dep == 2) gemm_bf3_kernel<F, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a);      \
-      else gemm_bf3_kernel<F, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                    \
-    }                                                                                 \
-  }                                                                                   \
-  break;
-    WH_FMT_SWITCH(f, WH_GB)
+#define WH_GB(BK, D1)                                                                 \
+  if (p.bm == 32) {                                                                   \
+    if (p.bn == 128) gemm_bf3_kernel<BK, 1, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
+    else if (dep == 3) gemm_bf3_kernel<BK, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);       \
+    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    else gemm_bf3_kernel<BK, 1, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
+  } else {                                                                            \
+    if (p.bn == 128) gemm_bf3_kernel<BK, 2, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
+    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    else gemm_bf3_kernel<BK, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
+  }
+    switch (bk) {
+    case BK_E4: WH_GB(BK_E4, 1) break;
+    case BK_I8: WH_GB(BK_I8, 1) break;
+    case BK_FP4: WH_GB(BK_FP4, 1) break;
+    case BK_NF4: WH_GB(BK_NF4, 1) break;
+    default: return hipErrorInvalidValue;
+    }
 #undef WH_GB
   } else if (p.bn == kRegBN) {
 #define WH_GR(F)                                                                      \

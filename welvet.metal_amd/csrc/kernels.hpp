@@ -79,7 +79,7 @@ void set_forward_path(int path);
 // 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
 // 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
 // block per row group; -1 = auto: 16 for the FP8 converter formats, else 0).
-// 10 split-x bf16 MFMA GEMM for FP8 E4M3 and Int8 (1 on), 11 its weight
+// 10 split-x bf16 MFMA GEMM for FP8 E4M3, Int8, FP4 and NF4 (1 on), 11 its weight
 // prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
 // width (0: 256 output columns, 1: 128).
 enum TuneKey {
