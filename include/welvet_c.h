@@ -169,13 +169,14 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *     4 eight [0]
  *   4 register-B MFMA GEMM for formats of <= 16 bits [1]
  *   5 its workgroups per CU [0 = 2]
- *   6 hardware FP8 conversions and integer Int8 decode instead of tables [1]
+ *   6 hardware FP8 / FP4 conversions and integer Int8 decode instead of
+ *     tables [1]
  *   7 byte-pair decode table for 4-bit formats [1]
  *   8 all-loads-in-flight rows per block: 0 = 8 / chunks per lane, or 1, 2,
  *     4, 8, 16 (at most 16 / chunks per lane; FP8, Int8, 4-bit, 8-bit table
  *     and half formats) [0]
  *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
- *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2, else 0) [-1]
+ *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2 and FP4, else 0) [-1]
  *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
  *     FP8 E4M3, Int8, FP4 and NF4 weights at batch > 4 [1]
  *   11 its weight prefetch depth in k stages: 1, 2, or 3 (batch <= 32) [1]

@@ -109,7 +109,7 @@ def test_every_gemv_shape_knob_launches(oracle):
     """Every (chunks per lane, rows per block) request, including ones with
     no kernel of their own, computes the forward (falls back, never skips)."""
     rng = np.random.default_rng(23)
-    cases = [(4, 300, 1024), (26, 257, 2048), (9, 64, 4096), (2, 40, 3072)]
+    cases = [(4, 300, 1024), (26, 257, 2048), (9, 64, 4096), (2, 40, 3072), (16, 130, 2048)]
     old = {k: pywelvet.set_tuning(k, 0) for k in ("cr", "gemv_rows")}
     try:
         for cr in range(5):
@@ -213,7 +213,7 @@ def test_gemm_session_repeat(oracle, dtype):
             assert_bit_equal(dW, rdW, f"dW iter {i}")
 
 
-@pytest.mark.parametrize("dtype", [1, 0, 4, 9, 26, 14, 12, 27, 20])
+@pytest.mark.parametrize("dtype", [1, 0, 4, 9, 26, 14, 12, 27, 20, 16])
 @pytest.mark.parametrize("batch", [1, 2, 5, 40])
 def test_backward(oracle, dtype, batch):
     """dX within tolerance of the f64 contract; dW bit-identical (sequential

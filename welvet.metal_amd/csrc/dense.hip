@@ -36,10 +36,11 @@ namespace {
 // layout read through a 256-entry table of value pairs (one read per byte);
 // FE4 / FE5 decode FP8 E4M3 / E5M2 with the hardware converts, reading the
 // store's decode-ready copy (codec.hpp kcode: the reference's quirks applied
-// at encode / SGD time); FI8 decodes Int8 by integer conversion.
+// at encode / SGD time); FI8 decodes Int8 by integer conversion; FF4 decodes
+// FP4 E2M1 with the hardware converts (exact for all 16 codes, no scale).
 enum Fmt {
   FL1, FL2, FL3, FL4, FL5, FL6, FL8, FH16, FB16, FI16, FU16, FF32, FI32, FU32, FI64, FU64, FC64,
-  FC128, FF64, FE4, FE5, FI8, FL4P, kNumFmt
+  FC128, FF64, FE4, FE5, FI8, FL4P, FF4, kNumFmt
 };
 
 int fmt_of(int dt) {
@@ -70,11 +71,11 @@ int fmt_of(int dt) {
 // Chunk = the unit one lane loads: kE elements in kW dwords.
 template <int F>
 struct FI {
-  static constexpr int kBits = F == FL1 ? 1 : F == FL2 ? 2 : F == FL3 ? 3 : (F == FL4 || F == FL4P) ? 4
+  static constexpr int kBits = F == FL1 ? 1 : F == FL2 ? 2 : F == FL3 ? 3 : (F == FL4 || F == FL4P || F == FF4) ? 4
                              : F == FL5 ? 5 : F == FL6 ? 6 : (F == FL8 || F == FE4 || F == FE5 || F == FI8) ? 8
                              : (F == FH16 || F == FB16 || F == FI16 || F == FU16) ? 16
                              : (F == FF32 || F == FI32 || F == FU32) ? 32 : F == FC128 ? 128 : 64;
-  static constexpr bool kLut = (kBits <= 8 && F != FE4 && F != FE5 && F != FI8) || F == FL4P;
+  static constexpr bool kLut = (kBits <= 8 && F != FE4 && F != FE5 && F != FI8 && F != FF4) || F == FL4P;
   static constexpr bool kPair = F == FL4P;
   // floats of LDS table: 2^bits values, or 256 value pairs
   static constexpr int kTable = kPair ? 512 : (kLut ? (1 << kBits) : 1);
@@ -104,7 +105,7 @@ int fmt_chunk_elems(int f) {
   switch (f) {
   case FL1: case FL2: case FL3: case FL4: case FL5: case FL6: return 32;
   case FL8: case FE4: case FE5: case FI8: return 16;
-  case FL4P: return 32;
+  case FL4P: case FF4: return 32;
   case FH16: case FB16: case FI16: case FU16: return 8;
   case FF32: case FI32: case FU32: return 4;
   case FC128: return 1;
@@ -172,7 +173,10 @@ __device__ inline typename FI<F>::Acc chunk_value(const uint32_t (&w)[FI<F>::kW]
     const uint32_t b = (w[e >> 3] >> (8 * ((e >> 1) & 3))) & 0xffu;
     return lut[2 * b + (e & 1)];
   } else if constexpr (I::kLut) return lut[chunk_code<I::kBits, I::kW>(w, e)];
-  else if constexpr (F == FE4 || F == FE5) {
+  else if constexpr (F == FF4) {
+    const f2 p = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[e >> 3] >> (8 * ((e >> 1) & 3)), 1.0f, 0);
+    return (e & 1) ? p[1] : p[0];
+  } else if constexpr (F == FE4 || F == FE5) {
     const uint32_t q = w[e >> 2];
     f2 p;
     if (F == FE4) p = (e & 2) ? __builtin_amdgcn_cvt_pk_f32_fp8(q, true) : __builtin_amdgcn_cvt_pk_f32_fp8(q, false);
@@ -225,6 +229,20 @@ __device__ inline void decode_chunk(const uint32_t (&w)[FI<F>::kW], typename FI<
       const f2 p = ((const f2 *)tab)[b];
       v[2 * j] = p[0];
       v[2 * j + 1] = p[1];
+    }
+  } else if constexpr (F == FF4) {
+    // byte j of the chunk holds elements 2j (low nibble) and 2j + 1
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f2 p[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 0),
+                       __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 1),
+                       __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 2),
+                       __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 3)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * i + 2 * j] = p[j][0];
+        v[8 * i + 2 * j + 1] = p[j][1];
+      }
     }
   } else {
 #pragma unroll
@@ -1504,7 +1522,7 @@ bool chunk_aligned(const DevStore &w, int64_t len) {
 // Formats whose batch-1 GEMV takes the rows-per-block knob.
 constexpr bool gemv_rows_knob(int f) {
   return f == FE4 || f == FE5 || f == FI8 || f == FL4P || f == FL4 || f == FL8 || f == FH16 ||
-         f == FB16;
+         f == FB16 || f == FF4;
 }
 
 // (chunks per lane, rows per block) shapes of the all-loads GEMV built in
@@ -1521,6 +1539,7 @@ int kernel_fmt(int dt) {
     if (dt == kFP8E4M3) return FE4;
     if (dt == kFP8E5M2) return FE5;
     if (dt == kInt8) return FI8;
+    if (dt == kFP4) return FF4;
   }
   if (f == FL4 && g_tune[kTunePairLut]) return FL4P;
   return f;
@@ -1627,7 +1646,7 @@ hipError_t gemv_dispatch(int batch, const GemvArgs &a, hipStream_t s) {
   case FL6: F(FL6); case FL8: F(FL8); case FH16: F(FH16); case FB16: F(FB16); case FI16: F(FI16);    \
   case FU16: F(FU16); case FF32: F(FF32); case FI32: F(FI32); case FU32: F(FU32); case FI64: F(FI64); \
   case FU64: F(FU64); case FC64: F(FC64); case FC128: F(FC128); case FF64: F(FF64);                  \
-  case FE4: F(FE4); case FE5: F(FE5); case FI8: F(FI8); case FL4P: F(FL4P);                          \
+  case FE4: F(FE4); case FE5: F(FE5); case FI8: F(FI8); case FL4P: F(FL4P); case FF4: F(FF4);        \
   default: return hipErrorInvalidValue;                                                              \
   }
 
@@ -1693,7 +1712,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       case 4: C = 8; break;
       default:
         while (C < 8 && (a.nchunks + 64 * C - 1) / (64 * C) > 4) C *= 2;
-        if ((f == FE4 || f == FE5 || f == FI8) && C == 1) Rauto = 4;
+        if ((f == FE4 || f == FE5 || f == FI8 || f == FF4) && C == 1) Rauto = 4;
         if ((f == FL4P || f == FL4) && a.nchunks <= 128) C = 2, Rauto = 4;
       }
       const int S = (a.nchunks + 64 * C - 1) / (64 * C);
@@ -1703,16 +1722,17 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         int R = 8 / C;
         const int rk = g_tune[kTuneGemvRows] ? g_tune[kTuneGemvRows] : Rauto;
         if (gemv_rows_knob(f) && gemv_pf_extra(C, rk)) R = rk;
-        // grid: one block per row group, or (knob / FP8 default) a fixed
-        // number of waves per CU walking the row groups, x loaded once each
-        // (the FP8 converter formats; others take one block per group)
+        // grid: one block per row group, or (knob / FP8 and FP4 default) a
+        // fixed number of waves per CU walking the row groups, x loaded once
+        // each (the hardware-converter formats; others take one block per
+        // group)
         const int ngroups = (a.N + R - 1) / R;
         int wpc = g_tune[kTuneGemvWaves];
-        if (wpc < 0) wpc = (f == FE4 || f == FE5) ? 16 : 0;
+        if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
         int blocks = ngroups;
         if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
 #define WH_PF(F)                                                                         \
-  if constexpr (F == FE4 || F == FE5) {                                                  \
+  if constexpr (F == FE4 || F == FE5 || F == FF4) {                                      \
     if (blocks < ngroups) {                                                              \
       if (C == 1 && R == 4) gemv_loop_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);  \
       else if (C == 1 && R == 8) gemv_loop_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a); \

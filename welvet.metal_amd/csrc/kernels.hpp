@@ -74,11 +74,12 @@ void set_forward_path(int path);
 // the previous value (-1 for an unknown key).
 // 4 register-B forward GEMM for <= 16-bit formats (1 on), 5 its workgroups
 // per CU (0 = 2).
-// 6 hardware FP8 converts / integer Int8 decode instead of tables (1 on),
+// 6 hardware FP8 / FP4 converts and integer Int8 decode instead of tables (1 on),
 // 7 pair table for 4-bit formats (1 on).
 // 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
 // 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
-// block per row group; -1 = auto: 16 for the FP8 converter formats, else 0).
+// block per row group; -1 = auto: 16 for the FP8 and FP4 converter formats,
+// else 0).
 // 10 split-x bf16 MFMA GEMM for FP8 E4M3, Int8, FP4 and NF4 (1 on), 11 its weight
 // prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
 // width (0: 256 output columns, 1: 128).
