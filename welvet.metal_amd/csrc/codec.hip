@@ -190,12 +190,25 @@ __device__ inline float sgd_value(uint64_t code, int64_t i, float g, double lr, 
   return (float)((double)old - lr * (double)g);
 }
 
+// True when an SGD launch must leave the weights alone: an earlier cell's
+// step stopped (*stop != 0), or this cell's gradient holds a non-finite value
+// (*bad != 0, found by the kernel that produced it), which then sets the
+// stop code for this and every later cell.
+__device__ inline bool sgd_stopped(int *stop, const int *bad, int bad_value) {
+  if (bad != nullptr && *bad != 0) {
+    if (stop != nullptr && blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(stop, 0, bad_value);
+    return true;
+  }
+  return stop != nullptr && *stop != 0;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body,
                                                        uint8_t *__restrict__ kbody, int64_t n,
                                                        const float *__restrict__ g, double lr,
-                                                       float scale, float minv, const int *stop) {
-  if (stop != nullptr && *stop != 0) return;
+                                                       float scale, float minv, int *stop,
+                                                       const int *bad, int bad_value) {
+  if (sgd_stopped(stop, bad, bad_value)) return;
   constexpr int bits = dtype_bits(DT);
   constexpr int U = unit_elems<DT>();
   const int64_t units = (n + U - 1) / U;
@@ -239,8 +252,8 @@ __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ bod
 // pinned to the f64 value its soft-double approximates).
 __global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ w, int64_t n,
                                                            const float *__restrict__ g, double lr,
-                                                           const int *stop) {
-  if (stop != nullptr && *stop != 0) return;
+                                                           int *stop, const int *bad, int bad_value) {
+  if (sgd_stopped(stop, bad, bad_value)) return;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads)
     w[i] = w[i] - lr * (double)g[i];
@@ -250,8 +263,8 @@ __global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ 
 // f32 first, then subtracted in f32.
 __global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w, int64_t n,
                                                            const float *__restrict__ g, double lr,
-                                                           const int *stop) {
-  if (stop != nullptr && *stop != 0) return;
+                                                           int *stop, const int *bad, int bad_value) {
+  if (sgd_stopped(stop, bad, bad_value)) return;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads) {
     const float step = (float)(lr * (double)g[i]);
@@ -327,20 +340,20 @@ hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s
 }
 
 hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
-                      float scale, float minv, const int *stop, hipStream_t s) {
+                      float scale, float minv, int *stop, const int *bad, int bad_value, hipStream_t s) {
   if ((dt == kFP8E4M3 || dt == kFP8E5M2) && kbody == nullptr) return hipErrorInvalidValue;
   if (dt == kFloat32) {
-    sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop);
+    sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop, bad, bad_value);
     return hipGetLastError();
   }
   if (dt == kFloat64) {
-    sgd_f64_kernel<<<grid_for(n), kThreads, 0, s>>>((double *)body, n, g, lr, stop);
+    sgd_f64_kernel<<<grid_for(n), kThreads, 0, s>>>((double *)body, n, g, lr, stop, bad, bad_value);
     return hipGetLastError();
   }
 #define WH_SGD(D)                                                                           \
   if constexpr (D != kFloat32 && D != kFloat64) {                                           \
     sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
-        body, kbody, n, g, lr, scale, minv, stop);                                          \
+        body, kbody, n, g, lr, scale, minv, stop, bad, bad_value);                          \
     return hipGetLastError();                                                               \
   } else {                                                                                  \
     return hipErrorInvalidValue;                                                            \

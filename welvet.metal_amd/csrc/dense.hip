@@ -1863,7 +1863,9 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   const int f = kernel_fmt(w.dtype);
   if (kernel_body(w, f) == nullptr) return hipErrorInvalidValue;
   if (ws_bytes < backward_workspace_bytes(w, batch)) return hipErrorInvalidValue;
-  if (route == 3) {
+  if (dX == nullptr) {
+    // no input gradient wanted (the first layer of a training step)
+  } else if (route == 3) {
 #define WH_DXG(D)                                                                         \
   dx_generic_kernel<D><<<blocks_for((int64_t)batch * w.cols), 256, 0, s>>>(w, batch, dpre, dX); \
   break;

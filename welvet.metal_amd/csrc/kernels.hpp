@@ -37,10 +37,13 @@ hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, uint8
 hipError_t launch_decode(int dt, const uint8_t *body, int64_t n, float scale, float minv, float *out,
                          hipStream_t s);
 hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s);
-// SGD with fixed-scale re-encode; a no-op when `stop` is non-null and *stop != 0.
-// FP8 formats also refresh the decode-ready copy kbody (required for them).
+// SGD with fixed-scale re-encode; a no-op when `stop` is non-null and
+// *stop != 0, or when `bad` is non-null and *bad != 0 (a non-finite gradient
+// found upstream; then *stop = bad_value if it was 0).  FP8 formats also
+// refresh the decode-ready copy kbody (required for them).
 hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
-                      float scale, float minv, const int *stop, hipStream_t s);
+                      float scale, float minv, int *stop, const int *bad, int bad_value,
+                      hipStream_t s);
 // *flag = value if g holds a non-finite element and *flag is still 0.
 hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s);
 
@@ -53,8 +56,8 @@ size_t backward_workspace_bytes(const DevStore &w, int batch);
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
                           int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
                           hipStream_t s);
-// dpre = gy * act'(pre); dX = dpre . W; dW = sum_b dpre^T x (sequential FMA);
-// flag |= 1 when dW holds a non-finite value.
+// dpre = gy * act'(pre); dX = dpre . W (skipped when dX is null); dW =
+// sum_b dpre^T x (sequential FMA); flag |= 1 when dW holds a non-finite value.
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
                            void *ws, size_t ws_bytes, hipStream_t s);

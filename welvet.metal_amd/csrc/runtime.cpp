@@ -194,7 +194,7 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
   } else if (flag) {
     return make_status(kInvalid, "weights: nonfinite gradient");
   }
-  WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, s));
+  WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, nullptr, 0, s));
   return ok();
 }
 

@@ -46,7 +46,7 @@ struct welvet_hip_grid {
   float *d_x = nullptr, *d_t = nullptr, *d_gy = nullptr;
   int64_t x_elems = 0, t_elems = 0, gy_elems = 0;
   double *d_loss = nullptr;
-  int *d_flag = nullptr;  // [0] backward dW flag, [1] SGD stop code
+  int *d_flag = nullptr;  // [1] SGD stop code, [2 + i] non-finite dW of tape entry i
   // tape of the last forward: cell index and the input it read
   std::vector<int> tape;
   std::vector<const float *> tape_in;
@@ -180,7 +180,7 @@ const float *tape_output(const Grid *g) { return g->cells[g->tape.back()].post; 
 welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr, double *loss,
                        hipStream_t s) {
   const int64_t ny = (int64_t)g->batch * out_width;
-  WH_HIP(hipMemsetAsync(g->d_flag, 0, 2 * sizeof(int), s));
+  WH_HIP(hipMemsetAsync(g->d_flag, 0, (2 + g->tape.size()) * sizeof(int), s));
   WH_HIP(launch_mse(tape_output(g), d_target, ny, g->d_loss, g->d_gy, g->ws, g->ws_bytes, s));
   // the gradient a step passes back must fit the step before it in the tape
   // (a remote hop can break the chain: dense::backward_f32 dense.cpp:171-178)
@@ -193,12 +193,15 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
       return make_status(kInvalid, "dense: bwd shape mismatch");
     }
   }
+  // The first entry's input gradient leaves the step unused (the step
+  // returns none), so its dX is not computed.  Each dW launch flags its own
+  // non-finite values, which the SGD of that cell reads.
   const float *gy = g->d_gy;
   for (int i = (int)g->tape.size() - 1; i >= 0; --i) {
     Grid::Cell &c = g->cells[g->tape[i]];
-    float *gx = g->gx[i & 1];
+    float *gx = i > 0 ? g->gx[i & 1] : nullptr;
     WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, g->dpre, gx, c.dW,
-                           g->d_flag, g->ws, g->ws_bytes, s));
+                           g->d_flag + 2 + i, g->ws, g->ws_bytes, s));
     gy = gx;
   }
   welvet_status late = ok();  // a host-side SGD error found part-way (codes after kernel codes)
@@ -207,17 +210,18 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   } else if (!std::isfinite(lr)) {
     late = make_status(kInvalid, "weights: bad SGD arguments");
   } else {
-    for (int idx : g->tape) {
-      Grid::Cell &c = g->cells[idx];
+    for (size_t j = 0; j < g->tape.size(); ++j) {
+      Grid::Cell &c = g->cells[g->tape[j]];
       const int64_t n = c.W.n();
+      const int code = c.W.dtype == kFloat32 ? kUnsupported : kInvalid;
       // the gradient check comes first, then the Float32 rate check (store_sgd order)
-      WH_HIP(launch_nonfinite(c.dW, n, g->d_flag + 1, c.W.dtype == kFloat32 ? kUnsupported : kInvalid,
-                              s));
       if (c.W.dtype == kFloat32 && (std::fabs(lr) > FLT_MAX || std::fabs(lr) < FLT_MIN)) {
+        WH_HIP(launch_nonfinite(c.dW, n, g->d_flag + 1, code, s));
         late = make_status(kUnsupported, "SGD: learning rate outside the f32 range");
         break;
       }
-      WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1, s));
+      WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1,
+                        g->d_flag + 2 + j, code, s));
     }
   }
   int stop = 0;
@@ -298,8 +302,8 @@ welvet_status welvet_hip_grid_new(int32_t depth, int32_t rows, int32_t cols, int
     return make_status(kInternal, "hip: %s", hipGetErrorString(e));
   };
   hipError_t e = hipMalloc(&g->d_loss, sizeof(double));
-  if (e == hipSuccess) e = hipMalloc(&g->d_flag, 2 * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(g->d_flag, 0, 2 * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&g->d_flag, (2 + (size_t)n) * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(g->d_flag, 0, (2 + (size_t)n) * sizeof(int));
   if (e != hipSuccess) return fail(e);
   st = grow_ws(g, mse_workspace_bytes(0));
   if (st.code) {
