@@ -75,7 +75,7 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(gemv_waves=2, gemv_rows=16, cr=3), dict(gemv_waves=1, gemv_rows=1, pair_lut=0),
          dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4), dict(bf3_depth=2),
          dict(bf3_depth=3), dict(bf3_depth=3, gemm_occ=1), dict(bf3_cols=1),
-         dict(bf3_cols=1, gemm_occ=1)]
+         dict(bf3_cols=1, gemm_occ=1), dict(dw_mfma=0)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -231,6 +231,37 @@ def test_backward(oracle, dtype, batch):
         dpre, rdX, rdW = oracle.backward(Wd, x, pre, gy, act)
         assert_close(dX, rdX, out, f"dX act={act}")
         assert_bit_equal(dW, rdW, f"dW act={act}")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 7, 64, 65])
+def test_dw_bit_exact_special_values(oracle, batch):
+    """dW stays the reference's sequential fmaf over the batch, bit for bit,
+    on both dW kernels, with signed zeros (ReLU passes -0 gradients), denormal
+    inputs and products across the exponent range, odd and even batches and
+    ragged tiles."""
+    rng = np.random.default_rng(131 + batch)
+    out, inn = 70, 130
+    W = rng.normal(0, 0.3, (out, inn)).astype(np.float32)
+    x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+    x[:, ::7] = -0.0
+    x[:, 3::11] = np.float32(1e-40) * np.sign(x[:, 3::11] + 0.5)
+    x[:, 5::13] *= np.float32(1e25)
+    gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    gy[:, ::5] = -0.0
+    gy[:, 2::9] *= np.float32(1e-25)
+    pre = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    Wd = oracle_weights(oracle, 1, W)
+    old = pywelvet.set_tuning("dw_mfma", 1)
+    try:
+        for knob in (1, 0):
+            pywelvet.set_tuning("dw_mfma", knob)
+            for act in (-1, 0):
+                with pywelvet.Session(W, batch=batch, act=act, dtype=1) as s:
+                    _, dW = s.backward(x, pre, gy)
+                _, _, rdW = oracle.backward(Wd, x, pre, gy, act)
+                assert_bit_equal(dW, rdW, f"dW dw_mfma={knob} act={act}")
+    finally:
+        pywelvet.set_tuning("dw_mfma", old)
 
 
 def test_backward_ragged(oracle):

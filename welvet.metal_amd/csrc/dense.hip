@@ -1460,6 +1460,98 @@ __global__ void __launch_bounds__(256) dw_kernel(const float *__restrict__ dpre,
   if (flag != nullptr && __any(bad) && (tid & 63) == 0) atomicOr(flag, 1);
 }
 
+// dW on the matrix cores with the reference's rounding.  Per output the
+// reference accumulates acc = fmaf(dpre[b][o], x[b][i], acc) over b in batch
+// order from 0 (welvet_dense.metal:155-178).  v_mfma_f32_32x32x2f32 computes
+// each output as fmaf(a1, b1, fmaf(a0, b0, c)): two fused multiply-adds in k
+// order, bit-identical to the VALU's fmaf (checked on the device over random
+// bit patterns, denormals, infinities, NaNs and signed zeros), so a chain of
+// them over k = batch rows reproduces the reference exactly.  An odd batch
+// ends with a -0 product, which leaves every accumulator (-0 included) as it
+// is.  Block: 128 (o) x 128 (i) outputs, four waves of 64 x 64 (2 x 2 tiles of
+// 32 x 32); lane (j, h) supplies batch row b + h of operand column j: the
+// A operand dpre[b][o0 + j], the B operand x[b][i0 + j] (coalesced 128-byte
+// rows).  Out-of-range rows and columns read a clamped valid element and are
+// never stored.
+__global__ void __launch_bounds__(256) dw_mfma_kernel(const float *__restrict__ dpre,
+                                                      const float *__restrict__ x, int B, int rows,
+                                                      int cols, float *__restrict__ dW, int *flag) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int o0 = blockIdx.y * 128 + (wave >> 1) * 64, i0 = blockIdx.x * 128 + (wave & 1) * 64;
+  const float *pa[2], *pb[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    pa[t] = dpre + min(o0 + 32 * t + j, rows - 1);
+    pb[t] = x + min(i0 + 32 * t + j, cols - 1);
+  }
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.0f;
+  // groups of kU k steps (2 kU batch rows); group g + 1's loads are in flight
+  // while group g's MFMAs run (two register sets).  Loads past the batch read
+  // row 0; the -0 / 0 padding replaces them where they are used (a select
+  // right after a load would make the compiler wait for that load at once).
+  constexpr int kU = 6;  // 24 loads per group: two groups fit the 63 loads a wave can have in flight
+  const int ng = (B + 2 * kU - 1) / (2 * kU);
+  auto load = [&](int g, float (&av)[kU][2], float (&bv)[kU][2]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int b = g * 2 * kU + 2 * u + h;
+      const int64_t bc = b < B ? b : 0;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        av[u][t] = pa[t][bc * rows];
+        bv[u][t] = pb[t][bc * cols];
+      }
+    }
+  };
+  auto mfmas = [&](int g, const float (&av)[kU][2], const float (&bv)[kU][2]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int b = g * 2 * kU + 2 * u;
+      if (b >= B) break;
+      const bool in = b + h < B;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(in ? av[u][mt] : -0.0f, in ? bv[u][nt] : 0.0f,
+                                                             acc[mt][nt], 0, 0, 0);
+    }
+  };
+  float a0[kU][2], b0v[kU][2], a1[kU][2], b1v[kU][2];
+  load(0, a0, b0v);
+  for (int g = 0; g < ng; g += 2) {
+    load(g + 1, a1, b1v);
+    mfmas(g, a0, b0v);
+    if (g + 1 >= ng) break;
+    load(g + 2, a0, b0v);
+    mfmas(g + 1, a1, b1v);
+  }
+  // D[m][n]: lane (j, h) holds column j, rows 8 (r / 4) + 4 h + r % 4
+  int bad = 0;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int i = i0 + 32 * nt + j;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = o0 + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (o < rows && i < cols) {
+          dW[(int64_t)o * cols + i] = acc[mt][nt][r];
+          bad |= !isfinite(acc[mt][nt][r]);
+        }
+      }
+    }
+  if (flag != nullptr && __any(bad) && lane == 0) atomicOr(flag, 1);
+}
+
 // ------------------------------------------------------------------ MSE
 __global__ void __launch_bounds__(256) mse_partial_kernel(const float *p, const float *t, int64_t n,
                                                           double *part) {
@@ -1496,7 +1588,7 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -1901,8 +1993,13 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dim3 g2((w.cols + 63) / 64, (w.rows + 63) / 64);
-  dw_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
+  if (g_tune[kTuneDwMfma]) {
+    dim3 g2((w.cols + 127) / 128, (w.rows + 127) / 128);
+    dw_mfma_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
+  } else {
+    dim3 g2((w.cols + 63) / 64, (w.rows + 63) / 64);
+    dw_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
+  }
   return hipGetLastError();
 }
 

@@ -85,11 +85,12 @@ void set_forward_path(int path);
 // else 0).
 // 10 split-x bf16 MFMA GEMM for FP8 E4M3, Int8, FP4 and NF4 (1 on), 11 its weight
 // prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
-// width (0: 256 output columns, 1: 128).
+// width (0: 256 output columns, 1: 128).  13 dW on the fp32 MFMA (1, bit-identical
+// to the sequential-FMA VALU kernel, 0).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
-  kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kNumTune = 13
+  kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kNumTune = 14
 };
 int set_tuning(int key, int value);
 
