@@ -420,6 +420,87 @@ __global__ void __launch_bounds__(1024) gemv1_kernel(GemvArgs a, int rows_per_bl
   }
 }
 
+// Lane exchanges without the LDS crossbar (f64 values as two dwords).
+// swap32: a <- [a lanes 0-31, b lanes 0-31], b <- [a lanes 32-63, b lanes 32-63]
+// (v_permlane32_swap); swap16: the same on 16-lane row pairs (rows 0/1, 2/3:
+// v_permlane16_swap); dpp<CTRL>: the value of the DPP partner lane
+// (0x140 row mirror i <-> 15 - i, 0x141 half-row mirror i <-> 7 - i, quad
+// permutes 0xB1 = xor 1, 0x4E = xor 2).
+typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+__device__ inline void swap32(double &a, double &b) {
+  const uint64_t ua = __builtin_bit_cast(uint64_t, a), ub = __builtin_bit_cast(uint64_t, b);
+  const u32x2v lo = __builtin_amdgcn_permlane32_swap((unsigned)ua, (unsigned)ub, false, false);
+  const u32x2v hi = __builtin_amdgcn_permlane32_swap((unsigned)(ua >> 32), (unsigned)(ub >> 32), false, false);
+  a = __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32));
+  b = __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+}
+__device__ inline void swap16(double &a, double &b) {
+  const uint64_t ua = __builtin_bit_cast(uint64_t, a), ub = __builtin_bit_cast(uint64_t, b);
+  const u32x2v lo = __builtin_amdgcn_permlane16_swap((unsigned)ua, (unsigned)ub, false, false);
+  const u32x2v hi = __builtin_amdgcn_permlane16_swap((unsigned)(ua >> 32), (unsigned)(ub >> 32), false, false);
+  a = __builtin_bit_cast(double, (uint64_t)lo[0] | ((uint64_t)hi[0] << 32));
+  b = __builtin_bit_cast(double, (uint64_t)lo[1] | ((uint64_t)hi[1] << 32));
+}
+template <int CTRL>
+__device__ inline double dpp(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const unsigned lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xf, 0xf, false);
+  const unsigned hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// Reduction of the batch-1 GEMV: acc[r] holds this lane's partial of row r.
+// log2(R) transposing steps (lane bit 5, 4, 3, 2: each lane keeps half of its
+// rows and adds the other half's partner values), then a sum over the lanes
+// left sharing a row.  Returns, on every lane l, the full sum of row
+// l >> (6 - log2 R).  Any pairing that counts each lane once gives the sum:
+// the mirrors pair lanes across the same bit boundary as an xor would.
+template <int R>
+__device__ inline double row_reduce(double (&acc)[R], int lane) {
+  constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
+  static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
+  if constexpr (LR >= 1) {
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) {
+      swap32(acc[i], acc[i + R / 2]);
+      acc[i] += acc[i + R / 2];
+    }
+  }
+  if constexpr (LR >= 2) {
+#pragma unroll
+    for (int i = 0; i < R / 4; ++i) {
+      swap16(acc[i], acc[i + R / 4]);
+      acc[i] += acc[i + R / 4];
+    }
+  }
+  if constexpr (LR >= 3) {
+    const bool hi = (lane >> 3) & 1;
+#pragma unroll
+    for (int i = 0; i < R / 8; ++i)
+      acc[i] = (hi ? acc[i + R / 8] : acc[i]) + dpp<0x140>(hi ? acc[i] : acc[i + R / 8]);
+  }
+  if constexpr (LR >= 4) {
+    const bool hi = (lane >> 2) & 1;
+    acc[0] = (hi ? acc[1] : acc[0]) + dpp<0x141>(hi ? acc[0] : acc[1]);
+  }
+  double v = acc[0];
+  if constexpr (LR == 0) {
+    double w = v;
+    swap32(v, w);
+    v += w;
+  }
+  if constexpr (LR <= 1) {
+    double w = v;
+    swap16(v, w);
+    v += w;
+  }
+  if constexpr (LR <= 2) v += dpp<0x140>(v);
+  if constexpr (LR <= 3) v += dpp<0x141>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0xB1>(v);
+  return v;
+}
+
 // Batch-1 GEMV with every load of a lane in flight at once.  A block owns R
 // rows; its S waves split the row into column slices of 64*C chunks (lane i
 // of a wave reads chunk slice*64*C + cc*64 + i of each row: 1 KB contiguous
@@ -518,22 +599,9 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
     }
     acc[r] = ((double)s[0] + (double)s[1]) + ((double)s[2] + (double)s[3]);
   }
-  // butterfly over the R rows: after log2(R) exchange steps on lane bits
-  // 5, 4, ... lane l holds a partial of row (l >> (6 - log2 R)); the
-  // remaining xor steps finish the 64-lane sum.
+  // lane l: the sum of row l >> (6 - log2 R) over the wave
   constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
-  static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
-#pragma unroll
-  for (int k = 0; k < LR; ++k) {
-    const int half = R >> (k + 1), bit = 5 - k;
-    const bool hi = (lane >> bit) & 1;
-#pragma unroll
-    for (int i = 0; i < half; ++i)
-      acc[i] = (hi ? acc[i + half] : acc[i]) + __shfl_xor(hi ? acc[i] : acc[i + half], 1 << bit);
-  }
-  double v = acc[0];
-#pragma unroll
-  for (int off = 32 >> LR; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const double v = row_reduce<R>(acc, lane);
   const int S = blockDim.x >> 6;
   if (S == 1) {
     if ((lane & ((64 >> LR) - 1)) == 0) {
@@ -669,20 +737,8 @@ __global__ void __launch_bounds__(256) gemv_loop_kernel(GemvArgs a) {
       }
       acc[r] = ((double)sm[0] + (double)sm[1]) + ((double)sm[2] + (double)sm[3]);
     }
-    // butterfly over the R rows: after log2(R) exchange steps on lane bits
-    // 5, 4, ... lane l holds a partial of row (l >> (6 - log2 R)); the
-    // remaining xor steps finish the 64-lane sum.
-#pragma unroll
-    for (int k = 0; k < LR; ++k) {
-      const int half = R >> (k + 1), bit = 5 - k;
-      const bool hi = (lane >> bit) & 1;
-#pragma unroll
-      for (int i = 0; i < half; ++i)
-        acc[i] = (hi ? acc[i + half] : acc[i]) + __shfl_xor(hi ? acc[i] : acc[i + half], 1 << bit);
-    }
-    double v = acc[0];
-#pragma unroll
-    for (int off = 32 >> LR; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    // lane l: the sum of row l >> (6 - log2 R) over the wave
+    const double v = row_reduce<R>(acc, lane);
     if (S == 1) {
       if ((lane & ((64 >> LR) - 1)) == 0) {
         const int row = r0 + (lane >> (6 - LR));
