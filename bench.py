@@ -39,7 +39,7 @@ METRIC = "Dense fwd HBM GB/s (batch 1) & TFLOP/s (batch 64), FP8/NF4 4096x11008"
 HBM_PEAK = 8000.0        # GB/s, MI355X
 FP32_MFMA_PEAK = 157.3   # TFLOP/s, MI355X dense fp32 matrix
 BF16_MFMA_PEAK = 2500.0  # TFLOP/s, MI355X dense bf16 matrix
-SPLIT_X_DTYPES = ("fp8e4m3", "int8", "fp4", "nf4")  # weights the split-x bf16 GEMM takes
+SPLIT_X_DTYPES = ("fp8e4m3", "fp8e5m2", "int8", "fp4", "nf4")  # weights the split-x bf16 GEMM takes
 IN, OUT = 4096, 11008
 MALL_BYTES = 512 << 20   # rotate past 2x the 256 MB Infinity Cache
 

@@ -178,7 +178,7 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
  *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2 and FP4, else 0) [-1]
  *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
- *     FP8 E4M3, Int8, FP4 and NF4 weights at batch > 4 [1]
+ *     FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4 [1]
  *   11 its weight prefetch depth in k stages: 1, 2, or 3 (batch <= 32) [1]
  *   12 its block width: 0 = 256 output columns, 1 = 128 [0]
  *   13 dW on the fp32 MFMA (bit-identical to the sequential-FMA VALU kernel:

@@ -157,6 +157,25 @@ def test_forward_headline_shapes(oracle, dtype, batch):
         check_forward(oracle, dtype, W, x)
 
 
+@pytest.mark.parametrize("batch", [1, 8, 40])
+def test_e5m2_nonfinite_weights(oracle, batch):
+    """E5M2 stores Inf for values past its range and a NaN code for NaN
+    (float_codecs.cpp:119-158): the products keep IEEE results (the split-x
+    GEMM, which cannot carry Inf * x exactly, is not used for such a store);
+    finite outputs within tolerance, non-finite ones identical in class."""
+    rng = np.random.default_rng(77 + batch)
+    W = rng.normal(0, 0.1, (70, 256)).astype(np.float32)
+    W[3, 5], W[10, 200], W[40, 7] = 1e6, -1e6, np.nan
+    x = rng.normal(0, 1, (batch, 256)).astype(np.float32)
+    pre, _ = pywelvet.forward(W, x, act=-1, dtype=5)
+    rpre, _ = oracle.forward(oracle_weights(oracle, 5, W), x, -1, None)
+    fin = np.isfinite(rpre)
+    assert not fin.all()
+    np.testing.assert_array_equal(np.isnan(pre), np.isnan(rpre))
+    np.testing.assert_array_equal(np.where(np.isinf(rpre), pre, 0), np.where(np.isinf(rpre), rpre, 0))
+    assert_close(np.where(fin, pre, 0), np.where(fin, rpre, 0), 256, "finite outputs")
+
+
 def test_session_reuse(oracle):
     rng = np.random.default_rng(3)
     W = rng.normal(0, 0.02, (300, 512)).astype(np.float32)

@@ -283,6 +283,14 @@ __global__ void __launch_bounds__(kThreads) nonfinite_kernel(const float *__rest
   if (__any(bad) && (threadIdx.x & 63) == 0) atomicCAS(flag, 0, value);
 }
 
+__global__ void __launch_bounds__(kThreads) e5m2_nonfinite_kernel(const uint8_t *__restrict__ c, int64_t n,
+                                                                  int *flag) {
+  int bad = 0;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    bad |= (c[i] & 0x7cu) == 0x7cu;
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
 }  // namespace
 
 #define WH_DTYPE_SWITCH(dt, F)                                                                    \
@@ -360,6 +368,11 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
   }
   WH_DTYPE_SWITCH(dt, WH_SGD)
 #undef WH_SGD
+}
+
+hipError_t launch_e5m2_nonfinite(const uint8_t *codes, int64_t n, int *flag, hipStream_t s) {
+  e5m2_nonfinite_kernel<<<grid_for(n / 16 + 1), kThreads, 0, s>>>(codes, n, flag);
+  return hipGetLastError();
 }
 
 hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s) {

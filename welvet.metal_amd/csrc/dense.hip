@@ -1080,13 +1080,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // Weight kinds the split-x GEMM takes.  Every decoded weight is exact in
 // bf16 once the per-tensor scale (applied by the reduction) is factored out:
-// E4M3 from the decode-ready copy, Int8 and FP4 codes as they are, and NF4
-// table values as three exact bf16 parts (hi + mid + lo, like x).
-enum Bf3Kind { BK_E4 = 0, BK_I8 = 1, BK_FP4 = 2, BK_NF4 = 3 };
+// E4M3 and E5M2 from the decode-ready copy, Int8 and FP4 codes as they are,
+// and NF4 table values as three exact bf16 parts (hi + mid + lo, like x).
+enum Bf3Kind { BK_E4 = 0, BK_I8 = 1, BK_FP4 = 2, BK_NF4 = 3, BK_E5 = 4 };
 
 template <int BK>
 struct B3 {
-  static constexpr int kBits = BK <= BK_I8 ? 8 : 4;
+  static constexpr int kBits = (BK <= BK_I8 || BK == BK_E5) ? 8 : 4;
   static constexpr int kWords = kBits;  // words of a lane's 32 weights per stage
   static constexpr int kParts = BK == BK_NF4 ? 3 : 1;
 };
@@ -1115,6 +1115,14 @@ __device__ inline void bf3_weights(const uint32_t *w, int q, const uint2 *t3, bf
         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+    parts[0] = bf16x8_of(u);
+  } else if constexpr (BK == BK_E5) {
+    const uint32_t w0 = w[2 * q], w1 = w[2 * q + 1];
+    const uint32_t u[4] = {
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w0, 1.0f, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w0, 1.0f, true)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w1, 1.0f, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w1, 1.0f, true))};
     parts[0] = bf16x8_of(u);
   } else if constexpr (BK == BK_I8) {
     uint32_t u[4];
@@ -1648,9 +1656,14 @@ int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
-int bf3_kind(int dt) {
+// Split-x weight kind of a store, -1 when the split-x GEMM does not take it.
+// E5M2 only while no stored code is Inf / NaN: x_part * Inf over the three
+// parts of x would give NaN where the fp32 product is Inf.
+int bf3_kind(const DevStore &w) {
+  const int dt = w.dtype;
   if (g_tune[kTuneBf3] == 0) return -1;
   if (dt == kFP8E4M3 && g_tune[kTuneFastDecode] != 0) return BK_E4;
+  if (dt == kFP8E5M2 && g_tune[kTuneFastDecode] != 0 && w.finite) return BK_E5;
   if (dt == kInt8) return BK_I8;
   if (dt == kFP4) return BK_FP4;
   if (dt == kNF4) return BK_NF4;
@@ -1746,8 +1759,8 @@ bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // format
 
 // Forward GEMM plan: the split-x bf16 kernel for the formats it takes, the
 // register-B kernel for other <= 16-bit formats, else the LDS-staged kernel.
-SkPlan plan_fwd_gemm(int f, int dt, int M, int K, int N) {
-  if (bf3_kind(dt) >= 0) {
+SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
+  if (bk >= 0) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
     const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
     SkPlan p = plan_sk(M, K, N, M <= 32 ? 32 : 64, bn, occ);
@@ -1826,7 +1839,7 @@ int set_tuning(int key, int value) {
 
 size_t forward_workspace_bytes(const DevStore &w, int batch) {
   if (fwd_route(w, batch) != 2) return 0;
-  return plan_fwd_gemm(kernel_fmt(w.dtype), w.dtype, batch, w.cols, w.rows).ws_bytes;
+  return plan_fwd_gemm(kernel_fmt(w.dtype), bf3_kind(w), batch, w.cols, w.rows).ws_bytes;
 }
 
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
@@ -1860,7 +1873,8 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       case 4: C = 8; break;
       default:
         while (C < 8 && (a.nchunks + 64 * C - 1) / (64 * C) > 4) C *= 2;
-        if ((f == FE4 || f == FE5 || f == FI8 || f == FF4) && C == 1) Rauto = 4;
+        if ((f == FE4 || f == FE5 || f == FI8) && C == 1) Rauto = 4;
+        if (f == FF4 && C == 1) Rauto = 8;
         if ((f == FL4P || f == FL4) && a.nchunks <= 128) C = 2, Rauto = 4;
       }
       const int S = (a.nchunks + 64 * C - 1) / (64 * C);
@@ -1932,14 +1946,14 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
     WH_FMT_SWITCH(f, WH_GV)
 #undef WH_GV
   }
-  const SkPlan p = plan_fwd_gemm(f, w.dtype, batch, w.cols, w.rows);
+  const int bk = bf3_kind(w);
+  const SkPlan p = plan_fwd_gemm(f, bk, batch, w.cols, w.rows);
   if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
   GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, batch, w.cols, w.rows, row_bytes_of(w),
              p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
   if (p.bf3) {
-    const int bk = bf3_kind(w.dtype);
     a.post = (bk == BK_I8 || bk == BK_NF4) ? w.scale : 1.0f;
-    if (bk == BK_E4) a.body = w.kbody;
+    if (bk == BK_E4 || bk == BK_E5) a.body = w.kbody;
     const int dep = g_tune[kTuneBf3Depth];
 #define WH_GB(BK, D1)                                                                 \
   if (p.bm == 32) {                                                                   \
@@ -1957,6 +1971,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
     case BK_I8: WH_GB(BK_I8, 1) break;
     case BK_FP4: WH_GB(BK_FP4, 1) break;
     case BK_NF4: WH_GB(BK_NF4, 1) break;
+    case BK_E5: WH_GB(BK_E5, 1) break;
     default: return hipErrorInvalidValue;
     }
 #undef WH_GB

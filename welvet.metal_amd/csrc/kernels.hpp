@@ -28,6 +28,7 @@ struct DevStore {
   const uint8_t *kbody;  // FP8 formats: decode-ready copy of body (codec.hpp kcode)
   const float *lut;  // 2^bits decoded values for formats of <= 8 bits
   float tab16[16];   // host copy of the first 16 table values
+  bool finite;       // no stored code decodes to Inf or NaN (known on the host)
 };
 
 // ---- codec.hip
@@ -46,6 +47,8 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
                       hipStream_t s);
 // *flag = value if g holds a non-finite element and *flag is still 0.
 hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s);
+// *flag |= 1 if one of the n FP8 E5M2 codes is Inf or NaN (exponent field all ones).
+hipError_t launch_e5m2_nonfinite(const uint8_t *codes, int64_t n, int *flag, hipStream_t s);
 
 // ---- dense.hip
 // Bytes of workspace the forward / backward launches below need.
@@ -83,7 +86,7 @@ void set_forward_path(int path);
 // 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
 // block per row group; -1 = auto: 16 for the FP8 and FP4 converter formats,
 // else 0).
-// 10 split-x bf16 MFMA GEMM for FP8 E4M3, Int8, FP4 and NF4 (1 on), 11 its weight
+// 10 split-x bf16 MFMA GEMM for FP8 E4M3 / E5M2, Int8, FP4 and NF4 (1 on), 11 its weight
 // prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
 // width (0: 256 output columns, 1: 128).  13 dW on the fp32 MFMA (1, bit-identical
 // to the sequential-FMA VALU kernel, 0).

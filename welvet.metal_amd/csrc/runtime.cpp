@@ -109,6 +109,7 @@ void free_store(Store *w) {
 struct EncodeScratch {
   Meta meta;
   Stats stats;
+  int nonfinite;
 };
 
 // WeightStore::make + encode_format_none (store.cpp:7-22, native_codec.cpp:819-833)
@@ -138,12 +139,19 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
   WH_HIP(hipMalloc(&scratch, sizeof(EncodeScratch)));
   hipError_t e = launch_encode(dtype, d_w, n, w->body, w->kbody, &scratch->meta, &scratch->stats, s);
   Meta m{};
+  int nonfinite = 0;
+  if (dtype == kFP8E5M2) {
+    if (e == hipSuccess) e = hipMemsetAsync(&scratch->nonfinite, 0, sizeof(int), s);
+    if (e == hipSuccess) e = launch_e5m2_nonfinite(w->kbody, n, &scratch->nonfinite, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(&nonfinite, &scratch->nonfinite, sizeof(int), hipMemcpyDeviceToHost, s);
+  }
   if (e == hipSuccess) e = hipMemcpyAsync(&m, &scratch->meta, sizeof(Meta), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   (void)hipFree(scratch);
   WH_HIP(e);
   w->scale = m.scale;
   w->minv = m.minv;
+  w->finite = nonfinite == 0;
   if (dtype_lut(dtype)) {
     WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
     WH_HIP(launch_lut(dtype, w->scale, w->minv, w->lut, s));
@@ -195,6 +203,7 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
     return make_status(kInvalid, "weights: nonfinite gradient");
   }
   WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, nullptr, 0, s));
+  if (w->dtype == kFP8E5M2) w->finite = false;  // an update can overflow to Inf
   return ok();
 }
 

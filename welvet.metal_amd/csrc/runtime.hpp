@@ -41,9 +41,12 @@ struct Store {
   int bias_len = 0;
 
   float tab16[16] = {};  // host copy of the first 16 decoded table values
+  // no code decodes to Inf / NaN: found at encode (FP8 E5M2 can hold them),
+  // cleared by an SGD step of a format that can produce them
+  bool finite = true;
 
   DevStore dev() const {
-    DevStore d{dtype, rows, cols, scale, minv, body, kbody, lut, {}};
+    DevStore d{dtype, rows, cols, scale, minv, body, kbody, lut, {}, finite};
     for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
     return d;
   }

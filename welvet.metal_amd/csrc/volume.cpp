@@ -222,6 +222,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
       }
       WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1,
                         g->d_flag + 2 + j, code, s));
+      if (c.W.dtype == kFP8E5M2) c.W.finite = false;  // an update can overflow to Inf
     }
   }
   int stop = 0;
