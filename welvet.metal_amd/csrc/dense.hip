@@ -1616,6 +1616,43 @@ __global__ void __launch_bounds__(256) dw_mfma_kernel(const float *__restrict__ 
   if (flag != nullptr && __any(bad) && lane == 0) atomicOr(flag, 1);
 }
 
+// out[c][r] = in[r][c] (bytes) through 64 x 64 LDS tiles: coalesced 16-byte
+// row reads, 16-byte writes along the output rows.
+__global__ void __launch_bounds__(256) transpose_u8_kernel(const uint8_t *__restrict__ in, int rows, int cols,
+                                                           uint8_t *__restrict__ out) {
+  __shared__ uint8_t t[64][64 + 4];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64, tid = threadIdx.x;
+  const int lr = tid >> 2, lc = (tid & 3) * 16;  // 64 rows x 4 pieces of 16 bytes
+  const int r = r0 + lr;
+  if (r < rows && c0 + lc + 16 <= cols && (cols & 15) == 0) {
+    const uint4 v = *(const uint4 *)(in + (int64_t)r * cols + c0 + lc);
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) t[lr][lc + j] = (uint8_t)(q[j >> 2] >> (8 * (j & 3)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int c = c0 + lc + j;
+      t[lr][lc + j] = (r < rows && c < cols) ? in[(int64_t)r * cols + c] : 0;
+    }
+  }
+  __syncthreads();
+  const int oc = c0 + lr;  // output row = input column
+  if (oc >= cols) return;
+  if (r0 + lc + 16 <= rows && (rows & 15) == 0) {
+    uint32_t q[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) q[j >> 2] |= (uint32_t)t[lc + j][lr] << (8 * (j & 3));
+    *(uint4 *)(out + (int64_t)oc * rows + r0 + lc) = make_uint4(q[0], q[1], q[2], q[3]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int orr = r0 + lc + j;
+      if (orr < rows) out[(int64_t)oc * rows + orr] = t[lc + j][lr];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ MSE
 __global__ void __launch_bounds__(256) mse_partial_kernel(const float *p, const float *t, int64_t n,
                                                           double *part) {
@@ -1842,6 +1879,32 @@ size_t forward_workspace_bytes(const DevStore &w, int batch) {
   return plan_fwd_gemm(kernel_fmt(w.dtype), bf3_kind(w), batch, w.cols, w.rows).ws_bytes;
 }
 
+// The split-x GEMM of plan p for weight kind bk (a.body, a.post set).
+hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
+  const int dep = g_tune[kTuneBf3Depth];
+#define WH_GB(BK, D1)                                                                 \
+  if (p.bm == 32) {                                                                   \
+    if (p.bn == 128) gemm_bf3_kernel<BK, 1, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
+    else if (dep == 3) gemm_bf3_kernel<BK, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);       \
+    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    else gemm_bf3_kernel<BK, 1, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
+  } else {                                                                            \
+    if (p.bn == 128) gemm_bf3_kernel<BK, 2, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
+    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    else gemm_bf3_kernel<BK, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
+  }
+  switch (bk) {
+  case BK_E4: WH_GB(BK_E4, 1) break;
+  case BK_I8: WH_GB(BK_I8, 1) break;
+  case BK_FP4: WH_GB(BK_FP4, 1) break;
+  case BK_NF4: WH_GB(BK_NF4, 1) break;
+  case BK_E5: WH_GB(BK_E5, 1) break;
+  default: return hipErrorInvalidValue;
+  }
+#undef WH_GB
+  return hipGetLastError();
+}
+
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
                           int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
                           hipStream_t s) {
@@ -1954,27 +2017,8 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   if (p.bf3) {
     a.post = (bk == BK_I8 || bk == BK_NF4) ? w.scale : 1.0f;
     if (bk == BK_E4 || bk == BK_E5) a.body = w.kbody;
-    const int dep = g_tune[kTuneBf3Depth];
-#define WH_GB(BK, D1)                                                                 \
-  if (p.bm == 32) {                                                                   \
-    if (p.bn == 128) gemm_bf3_kernel<BK, 1, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
-    else if (dep == 3) gemm_bf3_kernel<BK, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);       \
-    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
-    else gemm_bf3_kernel<BK, 1, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
-  } else {                                                                            \
-    if (p.bn == 128) gemm_bf3_kernel<BK, 2, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
-    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
-    else gemm_bf3_kernel<BK, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
-  }
-    switch (bk) {
-    case BK_E4: WH_GB(BK_E4, 1) break;
-    case BK_I8: WH_GB(BK_I8, 1) break;
-    case BK_FP4: WH_GB(BK_FP4, 1) break;
-    case BK_NF4: WH_GB(BK_NF4, 1) break;
-    case BK_E5: WH_GB(BK_E5, 1) break;
-    default: return hipErrorInvalidValue;
-    }
-#undef WH_GB
+    const hipError_t e = launch_bf3(p, bk, a, s);
+    if (e != hipSuccess) return e;
   } else if (p.bn == kRegBN) {
 #define WH_GR(F)                                                                      \
   if constexpr (FI<F>::kBits <= 16) {                                                 \
@@ -2005,13 +2049,30 @@ int dx_route(const DevStore &w, int batch) {
 }
 }  // namespace
 
+// dX of the GEMM route as a forward through W^T on the split-x GEMM: the
+// weight kinds of one byte per code whose transposed copy the store keeps
+// (-1 when dX takes the fp32 MFMA GEMM).
+int dx_bf3_kind(const DevStore &w, int batch) {
+  if (dx_route(w, batch) != 2 || w.rows % 16 != 0) return -1;
+  const int bk = bf3_kind(w);
+  return (bk == BK_E4 || bk == BK_E5 || bk == BK_I8) ? bk : -1;
+}
+
+bool backward_wants_transposed(const DevStore &w, int batch) { return dx_bf3_kind(w, batch) >= 0; }
+
 size_t backward_workspace_bytes(const DevStore &w, int batch) {
   const int route = dx_route(w, batch);
   if (route == 1) {
     const int nseg = (w.rows + kDxSegRows - 1) / kDxSegRows;
     return (size_t)nseg * batch * w.cols * sizeof(float);
   }
-  if (route == 2) return plan_sk(batch, w.rows, w.cols).ws_bytes;
+  if (route == 2) {
+    // either plan (the transposed copy may be refreshed after sizing)
+    size_t b = plan_sk(batch, w.rows, w.cols).ws_bytes;
+    const int bk = dx_bf3_kind(w, batch);
+    if (bk >= 0) b = std::max(b, plan_fwd_gemm(kernel_fmt(w.dtype), bk, batch, w.rows, w.cols).ws_bytes);
+    return b;
+  }
   return 0;
 }
 
@@ -2049,6 +2110,17 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     if (e != hipSuccess) return e;
     reduce_plain_kernel<<<blocks_for((int64_t)batch * w.cols), 256, 0, s>>>(
         (const float *)ws, nseg, (int64_t)batch * w.cols, dX);
+  } else if (dx_bf3_kind(w, batch) >= 0 && w.tbody != nullptr) {
+    // dX[b][i] = sum_o dpre[b][o] W[o][i]: the forward product through the
+    // transposed codes W^T [cols][rows] (rows bytes per row)
+    const int bk = dx_bf3_kind(w, batch);
+    const SkPlan p = plan_fwd_gemm(f, bk, batch, w.rows, w.cols);
+    GemmArgs a{w.tbody, w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, (int64_t)w.rows,
+               p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
+    a.post = bk == BK_I8 ? w.scale : 1.0f;
+    e = launch_bf3(p, bk, a, s);
+    if (e != hipSuccess) return e;
+    sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
   } else {
     const SkPlan p = plan_sk(batch, w.rows, w.cols);
     GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
@@ -2071,6 +2143,12 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     dim3 g2((w.cols + 63) / 64, (w.rows + 63) / 64);
     dw_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *out, hipStream_t s) {
+  const dim3 g((cols + 63) / 64, (rows + 63) / 64);
+  transpose_u8_kernel<<<g, 256, 0, s>>>(in, rows, cols, out);
   return hipGetLastError();
 }
 

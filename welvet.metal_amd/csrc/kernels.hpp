@@ -29,6 +29,9 @@ struct DevStore {
   const float *lut;  // 2^bits decoded values for formats of <= 8 bits
   float tab16[16];   // host copy of the first 16 table values
   bool finite;       // no stored code decodes to Inf or NaN (known on the host)
+  // codes of one byte (the decode-ready copy for FP8) transposed, [cols][rows],
+  // for dX on the split-x GEMM; null when absent or stale
+  const uint8_t *tbody;
 };
 
 // ---- codec.hip
@@ -59,6 +62,11 @@ size_t backward_workspace_bytes(const DevStore &w, int batch);
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
                           int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
                           hipStream_t s);
+// out[c][r] = in[r][c] for a rows x cols byte matrix.
+hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *out, hipStream_t s);
+// True when launch_backward's dX would use the store's transposed codes
+// (DevStore::tbody); the caller refreshes them before the launch.
+bool backward_wants_transposed(const DevStore &w, int batch);
 // dpre = gy * act'(pre); dX = dpre . W (skipped when dX is null); dW =
 // sum_b dpre^T x (sequential FMA); flag |= 1 when dW holds a non-finite value.
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,

@@ -97,12 +97,30 @@ const char *device_identity() {
 void free_store(Store *w) {
   if (w->body) (void)hipFree(w->body);
   if (w->kbody) (void)hipFree(w->kbody);
+  if (w->tbody) (void)hipFree(w->tbody);
+  w->tbody = nullptr;
+  w->tbody_ok = false;
   if (w->lut) (void)hipFree(w->lut);
   if (w->bias) (void)hipFree(w->bias);
   w->body = nullptr;
   w->kbody = nullptr;
   w->lut = nullptr;
   w->bias = nullptr;
+}
+
+welvet_status store_prepare_backward(Store *w, int batch, hipStream_t s) {
+  if (w->tbody_ok || !backward_wants_transposed(w->dev(), batch)) return ok();
+  const size_t bytes = (size_t)w->rows * w->cols;
+  if (w->tbody == nullptr) {
+    // padding: the GEMM's last 64-column stage may read past the last row
+    const size_t alloc = ((bytes + 64 + 255) / 256) * 256;
+    WH_HIP(hipMalloc(&w->tbody, alloc));
+    WH_HIP(hipMemsetAsync(w->tbody, 0, alloc, s));
+  }
+  const uint8_t *src = (w->dtype == kFP8E4M3 || w->dtype == kFP8E5M2) ? w->kbody : w->body;
+  WH_HIP(launch_transpose_u8(src, w->rows, w->cols, w->tbody, s));
+  w->tbody_ok = true;
+  return ok();
 }
 
 // Device scratch reused by encode: Meta + Stats.
@@ -204,6 +222,7 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
   }
   WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, nullptr, 0, s));
   if (w->dtype == kFP8E5M2) w->finite = false;  // an update can overflow to Inf
+  w->tbody_ok = false;
   return ok();
 }
 
@@ -357,6 +376,7 @@ welvet_status backward_device(welvet_dense_session *s, const float *d_x, const f
   WH_HIP(hipMalloc(&b->dX, nx * sizeof(float)));
   WH_HIP(hipMalloc(&b->dW, s->W.n() * sizeof(float)));
   welvet_status st = ensure_ws(s, backward_workspace_bytes(s->W.dev(), s->batch));
+  if (st.code == 0) st = store_prepare_backward(&s->W, s->batch, s->stream);
   if (st.code) return st;
   WH_HIP(hipMemsetAsync(s->d_flag, 0, sizeof(int), s->stream));
   WH_HIP(launch_backward(s->W.dev(), s->batch, d_x, d_pre, d_gy, s->act, b->dpre, b->dX, b->dW,

@@ -44,9 +44,12 @@ struct Store {
   // no code decodes to Inf / NaN: found at encode (FP8 E5M2 can hold them),
   // cleared by an SGD step of a format that can produce them
   bool finite = true;
+  // transposed codes for dX on the split-x GEMM (tbody_ok: current with body)
+  uint8_t *tbody = nullptr;
+  bool tbody_ok = false;
 
   DevStore dev() const {
-    DevStore d{dtype, rows, cols, scale, minv, body, kbody, lut, {}, finite};
+    DevStore d{dtype, rows, cols, scale, minv, body, kbody, lut, {}, finite, tbody_ok ? tbody : nullptr};
     for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
     return d;
   }
@@ -54,6 +57,8 @@ struct Store {
 };
 
 void free_store(Store *w);
+// Refreshes the transposed codes when a backward at this batch reads them.
+welvet_status store_prepare_backward(Store *w, int batch, hipStream_t s);
 // WeightStore::make on the device from f32 values already in HBM.
 welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d_w, hipStream_t s);
 welvet_status store_set_bias(Store *w, const double *bias, size_t bias_len, hipStream_t s);

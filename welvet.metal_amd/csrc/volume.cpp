@@ -200,6 +200,10 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   for (int i = (int)g->tape.size() - 1; i >= 0; --i) {
     Grid::Cell &c = g->cells[g->tape[i]];
     float *gx = i > 0 ? g->gx[i & 1] : nullptr;
+    if (gx != nullptr) {
+      welvet_status st = store_prepare_backward(&c.W, g->batch, s);
+      if (st.code) return st;
+    }
     WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, g->dpre, gx, c.dW,
                            g->d_flag + 2 + i, g->ws, g->ws_bytes, s));
     gy = gx;
@@ -223,6 +227,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
       WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1,
                         g->d_flag + 2 + j, code, s));
       if (c.W.dtype == kFP8E5M2) c.W.finite = false;  // an update can overflow to Inf
+      c.W.tbody_ok = false;
     }
   }
   int stop = 0;
