@@ -176,6 +176,29 @@ def test_e5m2_nonfinite_weights(oracle, batch):
     assert_close(np.where(fin, pre, 0), np.where(fin, rpre, 0), 256, "finite outputs")
 
 
+@pytest.mark.parametrize("batch", [5, 40])
+def test_backward_e5m2_nonfinite_weights(oracle, batch):
+    """dX through an E5M2 store holding Inf and NaN codes keeps the IEEE
+    products (the transposed split-x route is not used for it); dW does not
+    depend on the weights and stays bit-identical."""
+    rng = np.random.default_rng(91 + batch)
+    out, inn = 96, 160
+    W = rng.normal(0, 0.2, (out, inn)).astype(np.float32)
+    W[4, 9], W[50, 100], W[70, 3] = 1e6, -1e6, np.nan
+    x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+    gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    pre = rng.normal(0, 1, (batch, out)).astype(np.float32)
+    with pywelvet.Session(W, batch=batch, act=-1, dtype=5) as s:
+        dX, dW = s.backward(x, pre, gy)
+    _, rdX, rdW = oracle.backward(oracle_weights(oracle, 5, W), x, pre, gy, -1)
+    fin = np.isfinite(rdX)
+    assert not fin.all()
+    np.testing.assert_array_equal(np.isnan(dX), np.isnan(rdX))
+    np.testing.assert_array_equal(np.where(np.isinf(rdX), dX, 0), np.where(np.isinf(rdX), rdX, 0))
+    assert_close(np.where(fin, dX, 0), np.where(fin, rdX, 0), out, "finite dX")
+    assert_bit_equal(dW, rdW, "dW")
+
+
 def test_session_reuse(oracle):
     rng = np.random.default_rng(3)
     W = rng.normal(0, 0.02, (300, 512)).astype(np.float32)
@@ -232,7 +255,7 @@ def test_gemm_session_repeat(oracle, dtype):
             assert_bit_equal(dW, rdW, f"dW iter {i}")
 
 
-@pytest.mark.parametrize("dtype", [1, 0, 4, 9, 26, 14, 12, 27, 20, 16])
+@pytest.mark.parametrize("dtype", [1, 0, 4, 5, 9, 26, 14, 12, 27, 20, 16])
 @pytest.mark.parametrize("batch", [1, 2, 5, 40])
 def test_backward(oracle, dtype, batch):
     """dX within tolerance of the f64 contract; dW bit-identical (sequential
