@@ -254,29 +254,32 @@ def time_volume_train(torch, P, dims, widths, dtype, batch, steps, seed, lr=1e-3
             "sgd_skipped_nonfinite": sum(1 for c in codes if c)}
 
 
-def run_configs(torch, P):
-    """BASELINE configs 2-5 (config 1 is the reference's own CPU case)."""
+def run_configs(torch, P, only=("c2", "c3", "c4", "c5")):
+    """BASELINE configs 2-5 (config 1 is the reference's own CPU case); `only`
+    selects configs by name prefix."""
     out = {}
     seed = 0x5EED0000
-    for name, dt in (("e4m3", 4), ("e5m2", 5)):
+    for name, dt in (("e4m3", 4), ("e5m2", 5)) if "c2" in only else ():
         for b in (1, 32):
             out[f"c2_{name}_4096x4096_b{b}"] = time_volume_forward(
                 torch, P, [4096, 4096], dt, b, 100, 10, seed + 1)
-    for name, dt, init in (("nf4", 26, "normal"), ("fp4", 16, "normal"), ("fp4_u6", 16, "uniform6")):
+    for name, dt, init in (("nf4", 26, "normal"), ("fp4", 16, "normal"), ("fp4_u6", 16, "uniform6")) \
+            if "c3" in only else ():
         for b in (1, 8, 64):
             out[f"c3_{name}_4096-11008-4096_b{b}"] = time_volume_forward(
                 torch, P, [4096, 11008, 4096], dt, b, 50, 5, seed + 2, init=init)
-    for name, dt in (("int8", 9), ("e4m3", 4)):
+    for name, dt in (("int8", 9), ("e4m3", 4)) if "c4" in only else ():
         out[f"c4_{name}_2048-8192-2048_b256"] = time_volume_train(
             torch, P, (1, 1, 2, 1), [2048, 8192, 2048], dt, 256, 10, seed + 3)
     c5, skipped = {}, []
-    for dt in range(34):
+    for dt in range(34) if "c5" in only else ():
         r = time_volume_train(torch, P, (2, 2, 2, 4), [1024] * 33, dt, 16, 2, seed + 4)
         c5[P.DTYPE_NAMES[dt]] = round(r["ms_per_step"], 4)
         if r["sgd_skipped_nonfinite"]:
             skipped.append(P.DTYPE_NAMES[dt])
-    out["c5_2x2x2x4_1024_b16_ms_per_step"] = c5
-    out["c5_nonfinite_gradient_dtypes"] = skipped
+    if "c5" in only:
+        out["c5_2x2x2x4_1024_b16_ms_per_step"] = c5
+        out["c5_nonfinite_gradient_dtypes"] = skipped
     for k, v in out.items():
         if isinstance(v, dict) and "ms_per_step" in v:
             print(f"# {k}: {v['ms_per_step'] * 1e3:.1f} us/step  {v.get('tflops', 0):.2f} TFLOP/s",
@@ -313,6 +316,8 @@ def main():
     ap.add_argument("--only", default="", help="comma list of cases: fp8b1,nf4b1,fp8b64,nf4b64")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip BASELINE configs 2-5 (reported under config_results)")
+    ap.add_argument("--configs", default="c2,c3,c4,c5",
+                    help="comma list of the BASELINE configs to run: c2,c3,c4,c5")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (for scaling HBM counters)")
     a = ap.parse_args()
@@ -373,7 +378,7 @@ def main():
                     for k, v in results.items()},
     }
     if not a.no_configs:
-        line["config_results"] = run_configs(torch, pywelvet)
+        line["config_results"] = run_configs(torch, pywelvet, tuple(a.configs.split(",")))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(prim["weight_dtype"] == "nf4" and 26 or 4, prim["batch"])
     print(json.dumps(line), flush=True)
