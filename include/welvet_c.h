@@ -181,8 +181,10 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *     FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4 [1]
  *   11 its weight prefetch depth in k stages: 1, 2, or 3 (batch <= 32) [1]
  *   12 its block width: 0 = 256 output columns, 1 = 128 [0]
- *   13 dW on the fp32 MFMA (bit-identical to the sequential-FMA VALU kernel:
- *      the MFMA accumulates each product with fmaf rounding, in k order) [1] */
+ *   13 dW kernel, every one bit-identical to the sequential FMA (the fp32
+ *      MFMA accumulates each product with fmaf rounding, in k order): 2 MFMA
+ *      with operands staged in LDS (out and in multiples of 128, else 1),
+ *      1 MFMA with direct loads, 0 VALU [2] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

@@ -275,14 +275,15 @@ def test_backward(oracle, dtype, batch):
         assert_bit_equal(dW, rdW, f"dW act={act}")
 
 
+@pytest.mark.parametrize("shape", [(70, 130), (256, 384)], ids=["ragged", "tiled"])
 @pytest.mark.parametrize("batch", [1, 2, 3, 7, 64, 65])
-def test_dw_bit_exact_special_values(oracle, batch):
+def test_dw_bit_exact_special_values(oracle, batch, shape):
     """dW stays the reference's sequential fmaf over the batch, bit for bit,
-    on both dW kernels, with signed zeros (ReLU passes -0 gradients), denormal
-    inputs and products across the exponent range, odd and even batches and
-    ragged tiles."""
+    on every dW kernel (LDS-staged MFMA, direct MFMA, VALU), with signed zeros
+    (ReLU passes -0 gradients), denormal inputs and products across the
+    exponent range, odd and even batches, ragged and whole 128-tiles."""
     rng = np.random.default_rng(131 + batch)
-    out, inn = 70, 130
+    out, inn = shape
     W = rng.normal(0, 0.3, (out, inn)).astype(np.float32)
     x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
     x[:, ::7] = -0.0
@@ -295,7 +296,7 @@ def test_dw_bit_exact_special_values(oracle, batch):
     Wd = oracle_weights(oracle, 1, W)
     old = pywelvet.set_tuning("dw_mfma", 1)
     try:
-        for knob in (1, 0):
+        for knob in (2, 1, 0):
             pywelvet.set_tuning("dw_mfma", knob)
             for act in (-1, 0):
                 with pywelvet.Session(W, batch=batch, act=act, dtype=1) as s:

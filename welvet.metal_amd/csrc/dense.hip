@@ -1653,6 +1653,100 @@ __global__ void __launch_bounds__(256) transpose_u8_kernel(const uint8_t *__rest
   }
 }
 
+// dw_mfma_kernel with its operands staged through LDS (rows and columns
+// multiples of 128): per stage of 16 batch rows the block loads the dpre and
+// x panels (16 x 128 floats each) with coalesced 16-byte loads into a
+// double-buffered LDS ring, the next stage's loads in flight during this
+// stage's MFMAs.  Rows are padded to 160 floats so a wave's two k halves
+// (batch rows 2s and 2s + 1) read opposite bank halves.  Rows past the batch
+// hold the -0 / 0 padding.  Same MFMA chain, so the same bits as
+// dw_mfma_kernel.
+__global__ void __launch_bounds__(256) dw_mfma_lds_kernel(const float *__restrict__ dpre,
+                                                          const float *__restrict__ x, int B, int rows,
+                                                          int cols, float *__restrict__ dW, int *flag) {
+  constexpr int kS = 16, kRow = 160;
+  __shared__ float As[2][kS][kRow], Bs[2][kS][kRow];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int ob = blockIdx.y * 128, ib = blockIdx.x * 128;
+  const int wo = (wave >> 1) * 64, wi = (wave & 1) * 64;
+  // loader: thread t moves rows t / 32 and t / 32 + 8 of a panel, columns 4 (t % 32) .. + 3
+  const int lr = tid >> 5, lc = (tid & 31) * 4;
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.0f;
+  const int nstage = (B + kS - 1) / kS;
+  // stage st's panel rows for this thread (clamped into the batch: the
+  // padding replaces them in LDS)
+  const float *ga0 = dpre + ob + lc, *gb0 = x + ib + lc;
+  float4 ra0, ra1, rb0, rb1;
+  {
+    const int b0 = min(lr, B - 1), b1 = min(lr + 8, B - 1);
+    ra0 = *(const float4 *)(ga0 + (int64_t)b0 * rows);
+    ra1 = *(const float4 *)(ga0 + (int64_t)b1 * rows);
+    rb0 = *(const float4 *)(gb0 + (int64_t)b0 * cols);
+    rb1 = *(const float4 *)(gb0 + (int64_t)b1 * cols);
+  }
+  // component-wise selects (a select of whole float4 values becomes an
+  // indexed private array)
+  auto pad = [](bool in, float4 v, float p) {
+    return make_float4(in ? v.x : p, in ? v.y : p, in ? v.z : p, in ? v.w : p);
+  };
+  *(float4 *)&As[0][lr][lc] = pad(lr < B, ra0, -0.0f);
+  *(float4 *)&As[0][lr + 8][lc] = pad(lr + 8 < B, ra1, -0.0f);
+  *(float4 *)&Bs[0][lr][lc] = pad(lr < B, rb0, 0.0f);
+  *(float4 *)&Bs[0][lr + 8][lc] = pad(lr + 8 < B, rb1, 0.0f);
+  __syncthreads();
+  for (int st = 0; st < nstage; ++st) {
+    const int buf = st & 1;
+    const int sn = min(st + 1, nstage - 1);
+    {
+      const int b0 = min(sn * kS + lr, B - 1), b1 = min(sn * kS + lr + 8, B - 1);
+      ra0 = *(const float4 *)(ga0 + (int64_t)b0 * rows);
+      ra1 = *(const float4 *)(ga0 + (int64_t)b1 * rows);
+      rb0 = *(const float4 *)(gb0 + (int64_t)b0 * cols);
+      rb1 = *(const float4 *)(gb0 + (int64_t)b1 * cols);
+    }
+    // steps past the batch multiply the padding (adds -0: no change)
+#pragma unroll
+    for (int k = 0; k < kS / 2; ++k) {
+      const float a0 = As[buf][2 * k + h][wo + j], a1 = As[buf][2 * k + h][wo + 32 + j];
+      const float b0 = Bs[buf][2 * k + h][wi + j], b1 = Bs[buf][2 * k + h][wi + 32 + j];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    }
+    if (st + 1 < nstage) {
+      const int r0 = (st + 1) * kS + lr;
+      *(float4 *)&As[buf ^ 1][lr][lc] = pad(r0 < B, ra0, -0.0f);
+      *(float4 *)&As[buf ^ 1][lr + 8][lc] = pad(r0 + 8 < B, ra1, -0.0f);
+      *(float4 *)&Bs[buf ^ 1][lr][lc] = pad(r0 < B, rb0, 0.0f);
+      *(float4 *)&Bs[buf ^ 1][lr + 8][lc] = pad(r0 + 8 < B, rb1, 0.0f);
+    }
+    __syncthreads();
+  }
+  // D[m][n]: lane (j, h) holds column j, rows 8 (r / 4) + 4 h + r % 4
+  int bad = 0;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int i = ib + wi + 32 * nt + j;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = ob + wo + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+        dW[(int64_t)o * cols + i] = acc[mt][nt][r];
+        bad |= !isfinite(acc[mt][nt][r]);
+      }
+    }
+  if (flag != nullptr && __any(bad) && lane == 0) atomicOr(flag, 1);
+}
+
 // ------------------------------------------------------------------ MSE
 __global__ void __launch_bounds__(256) mse_partial_kernel(const float *p, const float *t, int64_t n,
                                                           double *part) {
@@ -1689,7 +1783,7 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 2};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -2136,7 +2230,10 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (g_tune[kTuneDwMfma]) {
+  if (g_tune[kTuneDwMfma] == 2 && w.rows % 128 == 0 && w.cols % 128 == 0) {
+    dim3 g2(w.cols / 128, w.rows / 128);
+    dw_mfma_lds_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
+  } else if (g_tune[kTuneDwMfma]) {
     dim3 g2((w.cols + 127) / 128, (w.rows + 127) / 128);
     dw_mfma_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
   } else {

@@ -96,8 +96,9 @@ void set_forward_path(int path);
 // else 0).
 // 10 split-x bf16 MFMA GEMM for FP8 E4M3 / E5M2, Int8, FP4 and NF4 (1 on), 11 its weight
 // prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
-// width (0: 256 output columns, 1: 128).  13 dW on the fp32 MFMA (1, bit-identical
-// to the sequential-FMA VALU kernel, 0).
+// width (0: 256 output columns, 1: 128).  13 dW kernel, all bit-identical to the
+// sequential FMA: 2 fp32 MFMA with operands staged in LDS (shapes of whole
+// 128-tiles; others take 1), 1 fp32 MFMA with direct loads, 0 VALU.
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
