@@ -144,6 +144,14 @@ WELVET_API welvet_status welvet_hip_volume_forward_device(welvet_hip_grid *g, co
 WELVET_API welvet_status welvet_hip_volume_train_step(welvet_hip_grid *g, const float *x,
                                                       int32_t in, const float *target, int32_t out,
                                                       double lr, double *loss, float *y);
+/* welvet_hip_volume_train_step that also returns runtime::backward::Result::
+ * grad_in (backward.cpp:125): grad_in [batch*in] (nullable) receives the input
+ * gradient of the first hop, which the WVN1 wire's WVNO reply carries
+ * (tools/dense_fwd/volume_fwd.cpp:1897-1902). */
+WELVET_API welvet_status welvet_hip_volume_train_step_grad(welvet_hip_grid *g, const float *x,
+                                                           int32_t in, const float *target,
+                                                           int32_t out, double lr, double *loss,
+                                                           float *y, float *grad_in);
 /* The same on device pointers on `stream`; returns after the step completed. */
 WELVET_API welvet_status welvet_hip_volume_train_step_device(welvet_hip_grid *g, const float *d_x,
                                                              int32_t in, const float *d_target,

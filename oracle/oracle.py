@@ -353,7 +353,10 @@ class Volume:
         return 0, "", cur, tape
 
     def train_step(self, x, target, lr):
-        """-> (code, message, loss, y)."""
+        """-> (code, message, loss, y).  After the backward, self.grad_in holds
+        backward::Result::grad_in (backward.cpp:125): the input gradient of
+        the first tape entry."""
+        self.grad_in = None
         code, msg, y, tape = self.forward(x)
         if code:
             return code, msg, 0.0, None
@@ -370,6 +373,7 @@ class Volume:
             _, dX, dW = self.O.backward(self.weights(co), inp, pre, gy, c["act"])
             grads[co] = dW
             gy = dX
+        self.grad_in = gy
         if lr == 0.0:
             return 1, "training: LR is 0", loss, y
         if not np.isfinite(lr):

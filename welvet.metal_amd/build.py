@@ -1,4 +1,5 @@
-"""Builds libwelvet_hip.so (HIP kernels + C ABI) for gfx950, in-tree.
+"""Builds libwelvet_hip.so (HIP kernels + C ABI) for gfx950, in-tree, and the
+wire tool welvet_dense_fwd (host C++ over the C ABI, linked to that library).
 
     python welvet.metal_amd/build.py            # build
     python welvet.metal_amd/build.py --jobs 8   # parallel object compiles
@@ -21,6 +22,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libwelvet_hip.so")
+TOOL = os.path.join(HERE, "welvet_dense_fwd")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+CXX = os.environ.get("CXX", "g++")
 SOURCES = ["codec.hip", "dense.hip", "runtime.cpp", "volume.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -58,7 +62,20 @@ def build(jobs: int = 3, verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_tool()
     return LIB
+
+
+def build_tool() -> str:
+    """The wire tool: host code only, finds the library next to itself."""
+    tmp = TOOL + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-Wall", "-I", INCLUDE, os.path.join(CSRC, "wire_tool.cpp"),
+           "-o", tmp, "-L", HERE, "-lwelvet_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"tool build failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, TOOL)
+    return TOOL
 
 
 if __name__ == "__main__":

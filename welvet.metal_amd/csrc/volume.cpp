@@ -176,9 +176,10 @@ const float *tape_output(const Grid *g) { return g->cells[g->tape.back()].post; 
 // training::step_dense after a forward: MSE loss and gradient, backward
 // through the tape in reverse, then SGD per cell in forward order.  Errors a
 // kernel finds (non-finite dW) stop every later cell's SGD on the device; the
-// host reads the first code once, at the end.
+// host reads the first code once, at the end.  grad_in (host, nullable)
+// receives backward::Result::grad_in, the first entry's input gradient.
 welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr, double *loss,
-                       hipStream_t s) {
+                       float *grad_in, hipStream_t s) {
   const int64_t ny = (int64_t)g->batch * out_width;
   WH_HIP(hipMemsetAsync(g->d_flag, 0, (2 + g->tape.size()) * sizeof(int), s));
   WH_HIP(launch_mse(tape_output(g), d_target, ny, g->d_loss, g->d_gy, g->ws, g->ws_bytes, s));
@@ -193,13 +194,13 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
       return make_status(kInvalid, "dense: bwd shape mismatch");
     }
   }
-  // The first entry's input gradient leaves the step unused (the step
-  // returns none), so its dX is not computed.  Each dW launch flags its own
-  // non-finite values, which the SGD of that cell reads.
+  // The first entry's input gradient is computed only when the caller asks
+  // for it (training::step_dense does not return it).  Each dW launch flags
+  // its own non-finite values, which the SGD of that cell reads.
   const float *gy = g->d_gy;
   for (int i = (int)g->tape.size() - 1; i >= 0; --i) {
     Grid::Cell &c = g->cells[g->tape[i]];
-    float *gx = i > 0 ? g->gx[i & 1] : nullptr;
+    float *gx = i > 0 || grad_in ? g->gx[i & 1] : nullptr;
     if (gx != nullptr) {
       welvet_status st = store_prepare_backward(&c.W, g->batch, s);
       if (st.code) return st;
@@ -208,6 +209,10 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
                            g->d_flag + 2 + i, g->ws, g->ws_bytes, s));
     gy = gx;
   }
+  if (grad_in)
+    WH_HIP(hipMemcpyAsync(grad_in, g->gx[0],
+                          (size_t)g->batch * g->cells[g->tape[0]].in * sizeof(float),
+                          hipMemcpyDeviceToHost, s));
   welvet_status late = ok();  // a host-side SGD error found part-way (codes after kernel codes)
   if (lr == 0.0) {
     late = make_status(kInvalid, "training: LR is 0");
@@ -428,6 +433,12 @@ welvet_status welvet_hip_volume_forward_device(welvet_hip_grid *g, const float *
 welvet_status welvet_hip_volume_train_step(welvet_hip_grid *g, const float *x, int32_t in,
                                            const float *target, int32_t out, double lr,
                                            double *loss, float *y) {
+  return welvet_hip_volume_train_step_grad(g, x, in, target, out, lr, loss, y, nullptr);
+}
+
+welvet_status welvet_hip_volume_train_step_grad(welvet_hip_grid *g, const float *x, int32_t in,
+                                                const float *target, int32_t out, double lr,
+                                                double *loss, float *y, float *grad_in) {
   if (!g || !loss) return make_status(kInvalid, "training: nil loss");
   if (!x || in <= 0) return make_status(kInvalid, "runtime.forward: empty input");
   std::lock_guard<std::mutex> lk(g->mu);
@@ -449,7 +460,7 @@ welvet_status welvet_hip_volume_train_step(welvet_hip_grid *g, const float *x, i
   if (y)
     WH_HIP(hipMemcpyAsync(y, tape_output(g), (size_t)g->batch * out * sizeof(float),
                           hipMemcpyDeviceToHost, g->stream));
-  return run_step(g, g->d_t, out, lr, loss, g->stream);
+  return run_step(g, g->d_t, out, lr, loss, grad_in, g->stream);
 }
 
 welvet_status welvet_hip_volume_train_step_device(welvet_hip_grid *g, const float *d_x, int32_t in,
@@ -467,7 +478,7 @@ welvet_status welvet_hip_volume_train_step_device(welvet_hip_grid *g, const floa
   const hipStream_t s = (hipStream_t)stream;
   st = run_forward(g, s);
   if (st.code) return st;
-  return run_step(g, d_target, out, lr, loss, s);
+  return run_step(g, d_target, out, lr, loss, nullptr, s);
 }
 
 welvet_status welvet_hip_grid_export_f32(welvet_hip_grid *g, int32_t z, int32_t y, int32_t x,
