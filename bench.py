@@ -302,6 +302,46 @@ def calibrate_copy(torch, mib: int = 256, launches: int = 5):
                                          "launches": launches}}), flush=True)
 
 
+def run_wire():
+    """The wire tool's own --bench framing, one tool process per wire: host
+    buffers in and out through the C ABI (PCIe-inclusive), the reference's
+    warm-ups.  WVD3 at the headline shape (mount = encode; execute = copy x
+    in, forward, copy pre/post out) and WVN1 at config 4 (each step rebuilds
+    the grid from the wire's f32 weights, as the reference's tool does)."""
+    import numpy as np
+    import wire
+
+    rng = np.random.default_rng(0x5EED00F0)
+    res = {}
+    W = rng.normal(0, 0.02, (OUT, IN)).astype(np.float32)
+    for name, dtype, batch in (("wvd3_fp8e4m3_b1", 4, 1), ("wvd3_nf4_b1", 26, 1),
+                               ("wvd3_fp8e4m3_b64", 4, 64)):
+        x = rng.normal(0, 1, (batch, IN)).astype(np.float32)
+        iters = 200
+        rc, out, err = wire.run(wire.wvd(W, x, dtype=dtype), f"--bench={iters}", timeout=300)
+        if rc:
+            raise RuntimeError(f"wire {name}: {err}")
+        b = wire.read_bench(wire.Reader(out))
+        res[name] = {"mount_ms": round(b["mount_ns"] / 1e6, 3),
+                     "exec_us": round(b["exec_ns"] / iters / 1e3, 2), "iters": iters}
+        print(f"# wire {name}: mount {res[name]['mount_ms']} ms, execute {res[name]['exec_us']} us",
+              file=sys.stderr, flush=True)
+    cells = {(0, 0, 0, 0): (_weights(rng, 8192, 2048, "normal"), 0, 9, None),
+             (0, 0, 1, 0): (_weights(rng, 2048, 8192, "normal"), -1, 9, None)}
+    x = rng.normal(0, 1, (256, 2048)).astype(np.float32)
+    t = rng.normal(0, 1, (256, 2048)).astype(np.float32)
+    iters = 10
+    rc, out, err = wire.run(wire.wvn((1, 1, 2, 1), 256, cells, x, t, 1e-3), f"--bench={iters}",
+                            timeout=300)
+    if rc:
+        raise RuntimeError(f"wire wvn1: {err}")
+    b = wire.read_bench(wire.Reader(out))
+    res["wvn1_c4_int8_b256"] = {"step_ms": round(b["ns"] / iters / 1e6, 3), "iters": iters}
+    print(f"# wire wvn1_c4_int8_b256: {res['wvn1_c4_int8_b256']['step_ms']} ms per rebuild + step",
+          file=sys.stderr, flush=True)
+    return res
+
+
 def pywelvet_name(dtype):
     import pywelvet
     return pywelvet.DTYPE_NAMES[dtype]
@@ -320,6 +360,8 @@ def main():
                     help="comma list of the BASELINE configs to run: c2,c3,c4,c5")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (for scaling HBM counters)")
+    ap.add_argument("--wire", action="store_true",
+                    help="run only the wire tool's --bench framing (host buffers; not the headline)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1",
@@ -328,6 +370,9 @@ def main():
     import torch
     if a.calibrate_copy:
         calibrate_copy(torch)
+        return
+    if a.wire:
+        print(json.dumps({"wire": run_wire()}), flush=True)
         return
     import pywelvet
 

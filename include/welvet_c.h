@@ -59,6 +59,26 @@ WELVET_API welvet_status welvet_dense_normalbp_f32(
     const float *grad_or_target, int32_t use_target, double lr, float *pre, float *post,
     float *dX, float *dW, float *W_after, double *loss);
 
+/* reference include/welvet_c.h:105-109 — SwiGLU forward (the WVS1 wire):
+ * Gate and Up [inter*in], Down [in*inter] row-major f32, each encoded into
+ * `dtype` as a Linear Dense layer without bias; x [batch*seq*in] ->
+ * pre = h = silu(Gate x) * (Up x) [batch*seq*inter], post = Down h
+ * [batch*seq*in] (src/layers/swiglu/swiglu.cpp:93-141). */
+WELVET_API welvet_status welvet_swiglu_forward_f32(int32_t batch, int32_t seq, int32_t input_dim,
+                                                   int32_t intermediate_dim, int32_t dtype,
+                                                   int32_t backend, const float *Gate,
+                                                   const float *Up, const float *Down,
+                                                   const float *x, float *pre, float *post);
+/* reference include/welvet_c.h:111-119 — SwiGLU NormalBP leaf: forward, the
+ * MSE gradient (use_target = 1) or grad_or_target as the output gradient,
+ * backward, SGD of Gate, Up, Down when lr != 0.  Outputs pre [batch*seq*inter],
+ * post and dX [batch*seq*in], dW and W_after = concat(Gate, Up, Down). */
+WELVET_API welvet_status welvet_swiglu_normalbp_f32(
+    int32_t batch, int32_t seq, int32_t input_dim, int32_t intermediate_dim, int32_t dtype,
+    int32_t backend, const float *Gate, const float *Up, const float *Down, const float *x,
+    const float *grad_or_target, int32_t use_target, double lr, float *pre, float *post, float *dX,
+    float *dW, float *W_after, double *loss);
+
 /* reference include/welvet_c.h:75-85 — resident session: the packed weights
  * and the [batch] activation buffers stay in HBM; batch is fixed at mount. */
 typedef struct welvet_dense_session welvet_dense_session;

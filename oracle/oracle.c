@@ -907,6 +907,25 @@ void or_dense_backward(int batch, int in, int out, int act, const double *Wd, co
 /* welvet_dense_normalbp_f32 c_abi.cpp:142-207 with the checks of
  * WeightStore::apply_sgd native_codec.cpp:909-945 and the Float32 launcher
  * training.mm:71-128.  Status codes: 0 ok, 1 invalid, 2 unsupported. */
+/* op_swiglu shaders/ops_common.metal:27-38.  c[1] == 0: d = act_value(a, SiLU) * b;
+ * c[1] == 1: e = d * act_value(a, SiLU), f = (d * b) * act_prime(a, SiLU) with
+ * d * b held in double-float (exact in f64) and one rounding to f32. */
+void or_swiglu_h(const float *gate, const float *up, int64_t n, float *h) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float s = or_act(gate[i], 1);
+    h[i] = s * up[i];
+  }
+}
+
+void or_swiglu_split(const float *gate, const float *up, const float *gh, int64_t n, float *d_up,
+                     float *d_gate) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float s = or_act(gate[i], 1);
+    d_up[i] = gh[i] * s;
+    d_gate[i] = (float)(((double)gh[i] * (double)up[i]) * (double)or_act_prime(gate[i], 1));
+  }
+}
+
 int or_normalbp(int batch, int in, int out, int act, int dtype, const float *W_init,
                 const double *bias, int64_t bias_len, const float *x, const float *grad_or_target,
                 int use_target, double lr, float *pre, float *post, float *dX, float *dW,

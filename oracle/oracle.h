@@ -28,6 +28,10 @@
  *                                      summation order exact) + the KAT
  *   or_act / or_act_prime              closed forms and finite differences
  *   or_mse / or_mse_grad               KAT (loss 0.15625) + closed forms
+ *   or_swiglu_h / or_swiglu_split      closed forms through the composed
+ *                                      SwiGLU layer (identity weights, swapped
+ *                                      roles distinguishable) and finite
+ *                                      differences of its forward (oracle.py)
  */
 #ifndef WELVET_ORACLE_H
 #define WELVET_ORACLE_H
@@ -86,6 +90,13 @@ void or_dense_forward(int batch, int in, int out, int act, const double *Wd, con
                       int64_t bias_len, const float *x, float *pre, float *post);
 void or_dense_backward(int batch, int in, int out, int act, const double *Wd, const float *x,
                        const float *pre, const float *gy, float *dpre, float *dX, float *dW);
+
+/* op_swiglu (shaders/ops_common.metal:27-38): forward h = fl32(silu(gate)) * up
+ * in f32; backward d_up = gh * fl32(silu(gate)) in f32 and
+ * d_gate = fl32(gh * up * fl32(silu'(gate))) with the product kept wide */
+void or_swiglu_h(const float *gate, const float *up, int64_t n, float *h);
+void or_swiglu_split(const float *gate, const float *up, const float *gh, int64_t n, float *d_up,
+                     float *d_gate);
 
 /* whole NormalBP leaf (src/interop/c_abi.cpp:142-207); returns a welvet status code */
 int or_normalbp(int batch, int in, int out, int act, int dtype, const float *W_init,

@@ -88,6 +88,10 @@ class Oracle:
         L.or_dense_forward_native.restype = None
         L.or_encode_many.argtypes = [_i, _vp, _i64, _vp]
         L.or_encode_many.restype = None
+        L.or_swiglu_h.argtypes = [_vp, _vp, _i64, _vp]
+        L.or_swiglu_h.restype = None
+        L.or_swiglu_split.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
+        L.or_swiglu_split.restype = None
 
     # -- codecs ---------------------------------------------------------------
     def native_bytes(self, dtype: int, n: int) -> int:
@@ -198,6 +202,73 @@ class Oracle:
         r["loss"] = loss.value
         r["status"] = st
         return r
+
+    # -- SwiGLU over Dense (src/layers/swiglu/swiglu.cpp) -------------------
+    def swiglu_h(self, gate, up):
+        gate = np.ascontiguousarray(gate, np.float32)
+        up = np.ascontiguousarray(up, np.float32)
+        h = np.zeros_like(gate)
+        self.lib.or_swiglu_h(_ptr(gate), _ptr(up), gate.size, _ptr(h))
+        return h
+
+    def swiglu_split(self, gate, up, gh):
+        gate, up, gh = (np.ascontiguousarray(a, np.float32) for a in (gate, up, gh))
+        d_up, d_gate = np.zeros_like(gate), np.zeros_like(gate)
+        self.lib.or_swiglu_split(_ptr(gate), _ptr(up), _ptr(gh), gate.size, _ptr(d_up),
+                                 _ptr(d_gate))
+        return d_up, d_gate
+
+    def swiglu_normalbp(self, dtype, Gate, Up, Down, x, grad_or_target=None, use_target=0,
+                        lr=0.0):
+        """welvet_swiglu_forward_f32 / welvet_swiglu_normalbp_f32
+        (c_abi.cpp:326-432) over swiglu.cpp:70-275: Gate/Up/Down Dense
+        layers (Linear, no bias) packed into `dtype`, forward h = silu(gate) *
+        up, post = Down h; backward through Down, op_swiglu, Gate and Up;
+        SGD Gate, Up, Down (the first error stops).  x is [rows][in] with
+        rows = batch * seq.  grad_or_target None = forward only.
+        -> dict(status, pre, post[, dX, dW, W_after, loss])."""
+        inter, inn = Gate.shape
+        x = np.ascontiguousarray(x, np.float32)
+        parts = []
+        for W in (Gate, Up, Down):
+            W = np.ascontiguousarray(W, np.float32)
+            raw, scale = self.pack(dtype, W)
+            parts.append([raw, scale, W.shape])
+        Wd = [self.decode_f64(dtype, r, sc, sh[0] * sh[1]).reshape(sh) for r, sc, sh in parts]
+        g_pre, _ = self.forward(Wd[0], x, -1)
+        u_pre, u_post = self.forward(Wd[1], x, -1)
+        h = self.swiglu_h(g_pre, u_post)
+        d_pre, post = self.forward(Wd[2], h, -1)
+        res = dict(status=0, pre=h, post=post)
+        if grad_or_target is None:
+            return res
+        t = np.ascontiguousarray(grad_or_target, np.float32).reshape(post.shape)
+        loss, gy = 0.0, t
+        if use_target:
+            loss, gy = self.mse(post, t), self.mse_grad(post, t)
+        _, grad_h, dW_d = self.backward(Wd[2], h, d_pre, gy, -1)
+        d_up, d_gate = self.swiglu_split(g_pre, u_post, grad_h)
+        _, gx_g, dW_g = self.backward(Wd[0], x, g_pre, d_gate, -1)
+        _, gx_u, dW_u = self.backward(Wd[1], x, u_pre, d_up, -1)
+        res.update(dX=gx_g + gx_u, dW=np.concatenate([dW_g.ravel(), dW_u.ravel(), dW_d.ravel()]),
+                   loss=loss)
+        if lr != 0.0:
+            for (raw, scale, sh), dW in zip(parts, (dW_g, dW_u, dW_d)):
+                n = sh[0] * sh[1]
+                if dtype == 1:
+                    if not np.all(np.isfinite(dW)):
+                        res["status"] = 2
+                        return res
+                    if abs(lr) > np.finfo(np.float32).max or abs(lr) < np.finfo(np.float32).tiny:
+                        res["status"] = 2
+                        return res
+                    self.sgd_f32(raw.view(np.float32), dW.ravel(), lr)
+                elif self.native_sgd(dtype, raw, scale, n, dW, lr):
+                    res["status"] = 1
+                    return res
+        res["W_after"] = np.concatenate([self.decode(dtype, r, sc, sh[0] * sh[1])
+                                         for r, sc, sh in parts])
+        return res
 
     def forward_native(self, dtype, raw, scale, x, out, inn, act, bias=None, threads=1):
         raw = np.ascontiguousarray(raw, np.uint8)

@@ -76,3 +76,15 @@ def test_argument_errors_before_device():
     assert L.welvet_hip_grid_new(1, 1, 1, 1, 0, ctypes.byref(h)).code == 1  # batch <= 0
     assert L.welvet_hip_grid_new(1, 1, 1, 1, 1, None).code == 1
     assert L.welvet_hip_volume_forward(None, None, 0, None, 0).code == 1
+
+
+def test_swiglu_argument_errors_before_device():
+    """c_abi.cpp:330-336, :369-381: dims and null checks come first."""
+    import numpy as np
+    G = np.ones((4, 2), np.float32)
+    D = np.ones((2, 4), np.float32)
+    st, _, _ = pywelvet.swiglu_forward(G, G, D, np.ones((0, 2), np.float32), status=True)
+    assert (st.code, st.message.decode()) == (1, "swiglu: invalid argument")
+    r = pywelvet.swiglu_normalbp(G, G, D, np.ones((1, 2), np.float32), np.zeros((1, 2)), 1, 0.1,
+                                 dtype=-1, status=True)
+    assert (r["status"].code, r["status"].message.decode()) == (1, "swiglu nbp: bad dtype -1")

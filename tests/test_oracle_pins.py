@@ -368,3 +368,74 @@ def test_forward_native_is_decode_then_forward(oracle, dtype):
         pre, post = oracle.forward_native(dtype, raw, scale, x, 33, 70, 3, bias, threads=threads)
         np.testing.assert_array_equal(pre, rpre)
         np.testing.assert_array_equal(post, rpost)
+
+
+# ------------------------------------------------------------ SwiGLU layer
+def _silu64(x):
+    x = np.asarray(x, np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def test_swiglu_identity_weights_closed_form(oracle):
+    """Gate = I, Up = c I, Down = I (Float64 stores hold them exactly): the
+    layer is post = h = fl32(silu(x)) * fl32(c x).  A swap of the roles of
+    gate and up (silu(c x) * x) or a missing silu would not match."""
+    rng = np.random.default_rng(21)
+    n, c = 24, np.float32(2.0)
+    x = rng.normal(0, 1.5, (3, n)).astype(np.float32)
+    I = np.eye(n, dtype=np.float32)
+    r = oracle.swiglu_normalbp(0, I, c * I, I, x)
+    want = _silu64(x).astype(np.float32) * (c * x)
+    np.testing.assert_array_equal(r["pre"], want)
+    np.testing.assert_array_equal(r["post"], want)
+    assert not np.allclose(want, _silu64(c * x).astype(np.float32) * x)
+
+
+def test_swiglu_backward_matches_finite_differences(oracle):
+    """dX and each third of dW (Gate, Up, Down in that order) against
+    central differences of L = sum(post * g) through the oracle's own forward,
+    Float64 weights; an O(1) mistake (sign, operand, order) fails by far."""
+    rng = np.random.default_rng(22)
+    inn, inter, rows = 6, 10, 2
+    G = rng.normal(0, 0.5, (inter, inn)).astype(np.float32)
+    U = rng.normal(0, 0.5, (inter, inn)).astype(np.float32)
+    D = rng.normal(0, 0.5, (inn, inter)).astype(np.float32)
+    x = rng.normal(0, 1, (rows, inn)).astype(np.float32)
+    g = rng.normal(0, 1, (rows, inn)).astype(np.float32)
+    r = oracle.swiglu_normalbp(0, G, U, D, x, g, 0, 0.0)
+
+    def L(G_, U_, D_, x_):
+        post = oracle.swiglu_normalbp(0, G_, U_, D_, x_)["post"].astype(np.float64)
+        return float(np.sum(post * g))
+
+    eps = 1e-2
+    def fd(arrs, k, idx):
+        a = [np.array(v, np.float32) for v in arrs]
+        hi, lo = [v.copy() for v in a], [v.copy() for v in a]
+        hi[k][idx] += eps
+        lo[k][idx] -= eps
+        return (L(*hi) - L(*lo)) / (2 * eps)
+
+    args = (G, U, D, x)
+    dW = r["dW"]
+    n_gu = inter * inn
+    for k, (arr, base) in enumerate(zip(args[:3], (0, n_gu, 2 * n_gu))):
+        for idx in [(0, 0), (arr.shape[0] - 1, arr.shape[1] - 1), (1, 2)]:
+            got = dW[base + idx[0] * arr.shape[1] + idx[1]]
+            want = fd(args, k, idx)
+            assert abs(got - want) <= 2e-3 * max(1.0, abs(want)), (k, idx, got, want)
+    for idx in [(0, 0), (1, inn - 1), (0, 3)]:
+        want = fd(args, 3, idx)
+        assert abs(r["dX"][idx] - want) <= 2e-3 * max(1.0, abs(want)), (idx, r["dX"][idx], want)
+
+
+def test_swiglu_split_elementwise_closed_form(oracle):
+    """op_swiglu's backward split at points where silu and silu' are known:
+    gate 0 gives silu 0 and silu' 1/2."""
+    gate = np.zeros(4, np.float32)
+    up = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    gh = np.array([2.0, 1.0, -4.0, 0.25], np.float32)
+    d_up, d_gate = oracle.swiglu_split(gate, up, gh)
+    np.testing.assert_array_equal(d_up, np.zeros(4, np.float32))
+    np.testing.assert_array_equal(d_gate, gh * up * np.float32(0.5))
+    np.testing.assert_array_equal(oracle.swiglu_h(gate, up), np.zeros(4, np.float32))

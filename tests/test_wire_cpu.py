@@ -30,7 +30,7 @@ def test_unknown_arg_and_empty_stdin():
 def test_bad_magic_and_other_layer_wires():
     rc, out, err = wire.run(b"ZZZZ")
     assert (rc, err.strip()) == (2, "welvet_dense_fwd: bad magic ZZZZ")
-    for m in (b"WVM1", b"WSB1", b"C2V1", b"MCG1"):
+    for m in (b"WVM1", b"WRB1", b"C2V1", b"MCG1"):
         rc, out, err = wire.run(m + b"\0" * 64)
         assert rc == 2 and out == b"" and "is not a Dense wire" in err, m
 
@@ -112,3 +112,23 @@ def test_wire_writers_round_trip():
     assert [r.i32() for _ in range(5)] == [1, 3, 2, 0, 9]
     np.testing.assert_array_equal(r.f32s(6), W.ravel())
     assert r.i32() == 0 and r.done()
+
+
+def test_swiglu_wire_parsing():
+    rc, out, err = wire.run(b"WVS1" + struct.pack("<3i", 1, 1, 4))
+    assert (rc, err.strip()) == (2, "welvet_dense_fwd: short WVS1 header")
+    rc, out, err = wire.run(b"WVS1" + struct.pack("<6i", 1, 0, 4, 8, 1, 0))
+    assert (rc, err.strip()) == (2, "welvet_dense_fwd: bad swiglu dims")
+    G = np.ones((8, 4), np.float32)
+    D = np.ones((4, 8), np.float32)
+    x = np.ones((2, 4), np.float32)
+    full = wire.wvs(G, G, D, x)
+    rc, out, err = wire.run(full[:60])
+    assert (rc, err.strip()) == (2, "welvet_dense_fwd: short WVS1 weights")
+    rc, out, err = wire.run(full[:-4])
+    assert (rc, err.strip()) == (2, "welvet_dense_fwd: short WVS1 input")
+    rc, out, err = wire.run(b"WSB1" + struct.pack("<2i", 1, 1))
+    assert (rc, err.strip()) == (2, "welvet_dense_fwd: short WSB1 header")
+    full = wire.wsb(G, G, D, x, np.zeros((2, 4)), 1, 0.1)
+    rc, out, err = wire.run(full[:-3])  # inside lr: silent exit 2 as the reference
+    assert (rc, out, err) == (2, b"", "")

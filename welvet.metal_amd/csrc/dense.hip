@@ -1780,6 +1780,39 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
     g[i] = (float)((((double)p[i] - (double)t[i]) * 2.0) / (double)n);
 }
 
+// --------------------------------------------------- SwiGLU element-wise
+// op_swiglu ops_common.metal:27-38, forward (c[1] == 0):
+//   h = fl32(silu(gate) * up), silu rounded to f32 first
+__global__ void __launch_bounds__(256) swiglu_fwd_kernel(const float *__restrict__ gate,
+                                                         const float *__restrict__ up, int64_t n,
+                                                         float *__restrict__ h) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    h[i] = act_value(gate[i], kSilu) * up[i];
+}
+
+// op_swiglu backward (c[1] == 1): d_up = fl32(gh * silu(gate));
+// d_gate = fl32((gh * up) * silu'(gate)), the product kept wide (exact in f64)
+// and rounded once
+__global__ void __launch_bounds__(256) swiglu_bwd_kernel(const float *__restrict__ gate,
+                                                         const float *__restrict__ up,
+                                                         const float *__restrict__ gh, int64_t n,
+                                                         float *__restrict__ d_up,
+                                                         float *__restrict__ d_gate) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const float g = gate[i], d = gh[i];
+    d_up[i] = d * act_value(g, kSilu);
+    d_gate[i] = (float)(((double)d * (double)up[i]) * (double)act_prime(g, kSilu));
+  }
+}
+
+// metal::add: out = fl32(a + b)
+__global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
+                                                  const float *__restrict__ b, int64_t n,
+                                                  float *__restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    out[i] = a[i] + b[i];
+}
+
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
@@ -2252,6 +2285,25 @@ hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *o
 size_t mse_workspace_bytes(int64_t n) {
   (void)n;
   return 1024 * sizeof(double);
+}
+
+hipError_t launch_swiglu_fwd(const float *gate, const float *up, int64_t n, float *h, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  swiglu_fwd_kernel<<<blocks_for(n), 256, 0, s>>>(gate, up, n, h);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *gh, int64_t n,
+                             float *d_up, float *d_gate, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  swiglu_bwd_kernel<<<blocks_for(n), 256, 0, s>>>(gate, up, gh, n, d_up, d_gate);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(const float *a, const float *b, int64_t n, float *out, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  add_kernel<<<blocks_for(n), 256, 0, s>>>(a, b, n, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_mse(const float *pred, const float *target, int64_t n, double *loss, float *grad,

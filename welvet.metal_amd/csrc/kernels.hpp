@@ -72,6 +72,13 @@ bool backward_wants_transposed(const DevStore &w, int batch);
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
                            void *ws, size_t ws_bytes, hipStream_t s);
+// SwiGLU element-wise steps (op_swiglu): h = fl32(silu(gate) * up);
+// backward d_up = fl32(gh * silu(gate)), d_gate = fl32(gh * up * silu'(gate)).
+hipError_t launch_swiglu_fwd(const float *gate, const float *up, int64_t n, float *h, hipStream_t s);
+hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *gh, int64_t n,
+                             float *d_up, float *d_gate, hipStream_t s);
+// out = fl32(a + b)
+hipError_t launch_add(const float *a, const float *b, int64_t n, float *out, hipStream_t s);
 // loss = sum (p - t)^2 / n (f64);  grad = fl32(2 (p - t) / n).
 hipError_t launch_mse(const float *pred, const float *target, int64_t n, double *loss, float *grad,
                       void *ws, size_t ws_bytes, hipStream_t s);

@@ -8,8 +8,11 @@
 //   WDB1 -> WDBO                      Dense NormalBP leaf        volume_fwd.cpp:1614-1757
 //   WVF1 -> WVFO                      volume forward             volume_fwd.cpp:130-207
 //   WVN1 -> WVNO                      volume NormalBP            volume_fwd.cpp:1759-1929
+//   WVS1 -> WVSO                      SwiGLU forward             main.cpp:650-720
+//   WSB1 -> WSBO                      SwiGLU NormalBP leaf       volume_fwd.cpp:2539-2690
 //   --bench=N                         WVB2 (mount_ns, exec_ns, iters) before WVO1 /
-//                                     WVFO; WVB1 (ns, iters) before WDBO / WVNO
+//                                     WVFO; WVB1 (ns, iters) before WDBO / WVNO /
+//                                     WVSO / WSBO
 //
 // Flags, messages and exit codes follow main.cpp:1253-1711: 2 for a short or
 // malformed wire, 1 for an error the library reports.  Wires of the
@@ -197,6 +200,108 @@ int run_dense_normalbp(int bench_iters) {
   welvet_status st = step();
   if (st.code != 0) return fail(st);
   if (!write_exact("WDBO", 4) || !write_counted(pre) || !write_counted(post) || !write_counted(dX) ||
+      !write_counted(dW) || !write_counted(W_after) || !write_one(loss))
+    return 2;
+  return 0;
+}
+
+// ---- WVS1 / WSB1: SwiGLU over three Dense layers ----------------------------
+struct SwigluWire {
+  int32_t batch = 0, seq = 0, in = 0, inter = 0, dtype = 1, backend = 0;
+  std::vector<float> gate, up, down, x;
+};
+
+// header and the three weight matrices (main.cpp:650-674,
+// volume_fwd.cpp:2539-2553); `tag` names the wire in the messages
+int read_swiglu(SwigluWire *w, const char *tag, bool check_dims) {
+  if (!read_one(&w->batch) || !read_one(&w->seq) || !read_one(&w->in) || !read_one(&w->inter) ||
+      !read_one(&w->dtype) || !read_one(&w->backend)) {
+    std::fprintf(stderr, "welvet_dense_fwd: short %s header\n", tag);
+    return 2;
+  }
+  if (check_dims && (w->batch <= 0 || w->seq <= 0 || w->in <= 0 || w->inter <= 0)) {
+    std::fprintf(stderr, "welvet_dense_fwd: bad swiglu dims\n");
+    return 2;
+  }
+  size_t nw = 0, rows = 0, nx = 0;
+  if (!elems(w->inter, w->in, &nw) || !elems(w->batch, w->seq, &rows) || !elems((int64_t)rows, w->in, &nx))
+    return 2;
+  if (!read_vec(w->gate, nw) || !read_vec(w->up, nw) || !read_vec(w->down, nw)) {
+    if (check_dims) std::fprintf(stderr, "welvet_dense_fwd: short %s weights\n", tag);
+    return 2;
+  }
+  if (!read_vec(w->x, nx)) {
+    if (check_dims) std::fprintf(stderr, "welvet_dense_fwd: short %s input\n", tag);
+    return 2;
+  }
+  return 0;
+}
+
+// WVS1 -> WVSO (main.cpp:650-720): --bench gives WVB1 before the reply
+int run_swiglu(int bench_iters) {
+  SwigluWire w;
+  if (int rc = read_swiglu(&w, "WVS1", true)) return rc;
+  std::vector<float> pre((size_t)w.batch * w.seq * w.inter), post(w.x.size());
+  auto once = [&]() {
+    return welvet_swiglu_forward_f32(w.batch, w.seq, w.in, w.inter, w.dtype, w.backend, w.gate.data(),
+                                     w.up.data(), w.down.data(), w.x.data(), pre.data(), post.data());
+  };
+  if (bench_iters > 0) {
+    for (int i = 0; i < 3; ++i) {
+      welvet_status st = once();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t0 = Clock::now();
+    for (int i = 0; i < bench_iters; ++i) {
+      welvet_status st = once();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t1 = Clock::now();
+    if (!write_exact("WVB1", 4) || !write_one(ns_between(t0, t1)) || !write_one((int32_t)bench_iters))
+      return 2;
+  } else {
+    welvet_status st = once();
+    if (st.code != 0) return fail(st);
+  }
+  return write_exact("WVSO", 4) && write_counted(pre) && write_counted(post) ? 0 : 2;
+}
+
+// WSB1 -> WSBO (volume_fwd.cpp:2539-2690): one SwiGLU NormalBP step from the
+// wire's weights; --bench gives WVB1, then the exported step
+int run_swiglu_normalbp(int bench_iters) {
+  SwigluWire w;
+  if (int rc = read_swiglu(&w, "WSB1", false)) return rc;
+  int32_t use_target = 0;
+  double lr = 0.0;
+  std::vector<float> gyt;
+  if (!read_one(&use_target) || !read_vec(gyt, w.x.size()) || !read_one(&lr)) return 2;
+  const size_t nw = 3 * (size_t)w.inter * w.in;
+  std::vector<float> pre((size_t)w.batch * w.seq * w.inter), post(w.x.size()), dX(w.x.size()),
+      dW(nw), W_after(nw);
+  double loss = 0.0;
+  auto step = [&]() {
+    return welvet_swiglu_normalbp_f32(w.batch, w.seq, w.in, w.inter, w.dtype, w.backend,
+                                      w.gate.data(), w.up.data(), w.down.data(), w.x.data(),
+                                      gyt.data(), use_target, lr, pre.data(), post.data(), dX.data(),
+                                      dW.data(), W_after.data(), &loss);
+  };
+  if (bench_iters > 0) {
+    for (int i = 0; i < 3; ++i) {
+      welvet_status st = step();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t0 = Clock::now();
+    for (int i = 0; i < bench_iters; ++i) {
+      welvet_status st = step();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t1 = Clock::now();
+    if (!write_exact("WVB1", 4) || !write_one(ns_between(t0, t1)) || !write_one((int32_t)bench_iters))
+      return 2;
+  }
+  welvet_status st = step();
+  if (st.code != 0) return fail(st);
+  if (!write_exact("WSBO", 4) || !write_counted(pre) || !write_counted(post) || !write_counted(dX) ||
       !write_counted(dW) || !write_counted(W_after) || !write_one(loss))
     return 2;
   return 0;
@@ -423,18 +528,18 @@ void usage() {
   std::fprintf(stderr,
                "welvet_dense_fwd (welvet.metal_amd, HIP gfx950; Dense wires)\n"
                "  --version | --identity | --gaps | --help\n"
-               "  --bench=N → WVB2 mount_ns+exec_ns (WVD, WVF1) | WVB1 ns (WDB1, WVN1)\n"
-               "  stdin WVD3/WVD2/WVD1→WVO1 | WVF1→WVFO\n"
-               "       WDB1→WDBO | WVN1→WVNO (Dense NormalBP)\n");
+               "  --bench=N → WVB2 mount_ns+exec_ns (WVD, WVF1) | WVB1 ns (WDB1, WVN1, WVS1, WSB1)\n"
+               "  stdin WVD3/WVD2/WVD1→WVO1 | WVF1→WVFO | WVS1→WVSO (SwiGLU)\n"
+               "       WDB1→WDBO | WVN1→WVNO (Dense NormalBP) | WSB1→WSBO (SwiGLU NormalBP)\n");
 }
 
 // the reference's wires of other layer kinds (main.cpp:1308-1700): recognised
 // so that a harness sees a clear refusal instead of "bad magic"
 bool other_layer_wire(const char *m) {
   static const char *kOther[] = {
-      "WVM1", "WVS1", "WVR1", "WVL1", "WSM1", "WEM1", "WSQ1", "WRE1", "WSX1", "WVC1", "WVC2",
+      "WVM1", "WVR1", "WVL1", "WSM1", "WEM1", "WSQ1", "WRE1", "WSX1", "WVC1", "WVC2",
       "WVC3", "WVT1", "WVT2", "WVT3", "WRN1", "WLS1", "WGD1", "WMB1", "WKM1", "WPL1", "WMC1",
-      "WRB1", "WRV1", "WLB1", "WLV1", "WSB1", "WSV1", "WXB1", "WXV1", "WEB1", "WEV1", "WHB1",
+      "WRB1", "WRV1", "WLB1", "WLV1", "WSV1", "WXB1", "WXV1", "WEB1", "WEV1", "WHB1",
       "WHV1", "C1B1", "C2B1", "C3B1", "C1V1", "C2V1", "C3V1", "T1B1", "T2B1", "T3B1", "T1V1",
       "T2V1", "T3V1", "RNB1", "RNV1", "LSB1", "LSV1", "SQB1", "SQV1", "REB1", "REV1", "MBB1",
       "MBV1", "MCB1", "MCV1", "GDB1", "GDV1", "STKB", "STKV", "STB1", "MBP1", "WMV1", "WRF1",
@@ -490,6 +595,8 @@ int main(int argc, char **argv) {
   if (std::memcmp(magic, "WVF1", 4) == 0) return run_volume_dense_fwd(bench_iters);
   if (std::memcmp(magic, "WDB1", 4) == 0) return run_dense_normalbp(bench_iters);
   if (std::memcmp(magic, "WVN1", 4) == 0) return run_volume_normalbp(bench_iters);
+  if (std::memcmp(magic, "WVS1", 4) == 0) return run_swiglu(bench_iters);
+  if (std::memcmp(magic, "WSB1", 4) == 0) return run_swiglu_normalbp(bench_iters);
   const bool v3 = std::memcmp(magic, "WVD3", 4) == 0;
   const bool v2 = std::memcmp(magic, "WVD2", 4) == 0;
   const bool v1 = std::memcmp(magic, "WVD1", 4) == 0;

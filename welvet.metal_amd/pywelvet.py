@@ -79,6 +79,14 @@ def lib() -> C.CDLL:
         L.welvet_dense_forward_f32.restype = Status
         L.welvet_dense_normalbp_f32.argtypes = prefix + [_f, _i32, C.c_double] + [_f] * 5 + [_d]
         L.welvet_dense_normalbp_f32.restype = Status
+        sw = [_i32] * 6 + [_f] * 4
+        L.welvet_swiglu_forward_f32.argtypes = sw + [_f, _f]
+        L.welvet_swiglu_forward_f32.restype = Status
+        L.welvet_swiglu_normalbp_f32.argtypes = sw + [_f, _i32, C.c_double] + [_f] * 5 + [_d]
+        L.welvet_swiglu_normalbp_f32.restype = Status
+        L.welvet_hip_volume_train_step_grad.argtypes = [_vp, _f, _i32, _f, _i32, C.c_double, _d,
+                                                        _f, _f]
+        L.welvet_hip_volume_train_step_grad.restype = Status
         L.welvet_dense_mount.argtypes = [_i32] * 5 + [_f, _d, C.c_size_t, C.POINTER(_vp)]
         L.welvet_dense_mount.restype = Status
         L.welvet_dense_execute.argtypes = [_vp, _f, _f, _f]
@@ -204,6 +212,44 @@ def normalbp(W, x, grad_or_target, use_target, lr, act=-1, dtype=1, bias=None, s
                                          int(use_target), lr, _fp(r["pre"]), _fp(r["post"]),
                                          _fp(r["dX"]), _fp(r["dW"]), _fp(r["W_after"]),
                                          C.byref(loss))
+    r["loss"] = loss.value
+    if status:
+        r["status"] = st
+        return r
+    check(st)
+    return r
+
+
+def swiglu_forward(Gate, Up, Down, x, dtype=1, seq=1, status=False):
+    """welvet_swiglu_forward_f32; x [batch*seq][in] -> (pre = h, post)."""
+    Gate, Up, Down, x = _f32(Gate), _f32(Up), _f32(Down), _f32(x)
+    inter, inn = Gate.shape
+    rows = x.shape[0]
+    pre = np.zeros((rows, inter), np.float32)
+    post = np.zeros((rows, inn), np.float32)
+    st = lib().welvet_swiglu_forward_f32(rows // seq, seq, inn, inter, dtype, 0, _fp(Gate), _fp(Up),
+                                         _fp(Down), _fp(x), _fp(pre), _fp(post))
+    if status:
+        return st, pre, post
+    check(st)
+    return pre, post
+
+
+def swiglu_normalbp(Gate, Up, Down, x, grad_or_target, use_target, lr, dtype=1, seq=1,
+                    status=False):
+    """welvet_swiglu_normalbp_f32 -> dict(pre, post, dX, dW, W_after, loss)."""
+    Gate, Up, Down, x, g = _f32(Gate), _f32(Up), _f32(Down), _f32(x), _f32(grad_or_target)
+    inter, inn = Gate.shape
+    rows = x.shape[0]
+    nw = 3 * inter * inn
+    r = dict(pre=np.zeros((rows, inter), np.float32), post=np.zeros((rows, inn), np.float32),
+             dX=np.zeros((rows, inn), np.float32), dW=np.zeros(nw, np.float32),
+             W_after=np.zeros(nw, np.float32))
+    loss = C.c_double()
+    st = lib().welvet_swiglu_normalbp_f32(rows // seq, seq, inn, inter, dtype, 0, _fp(Gate), _fp(Up),
+                                          _fp(Down), _fp(x), _fp(g), int(use_target), lr,
+                                          _fp(r["pre"]), _fp(r["post"]), _fp(r["dX"]), _fp(r["dW"]),
+                                          _fp(r["W_after"]), C.byref(loss))
     r["loss"] = loss.value
     if status:
         r["status"] = st

@@ -17,6 +17,12 @@ build's tool of the same name.
   WVN1      WVF1's body, then target [batch*out_last] f32 and lr f64
             -> WVNO loss f64; n, grad_in; n_cells; per enabled cell out, in,
             W_after; n, y               tools/dense_fwd/volume_fwd.cpp:1759-1929
+  WVS1      batch, seq, in, inter, dtype, backend i32; Gate, Up [inter*in],
+            Down [in*inter] f32; x [batch*seq*in]
+            -> WVSO (n, values) for pre (h), post   tools/dense_fwd/main.cpp:650-720
+  WSB1      WVS1's fields, then use_target i32; grad_or_target [batch*seq*in];
+            lr f64 -> WSBO as WDBO (dW, W_after = concat(Gate, Up, Down))
+            tools/dense_fwd/volume_fwd.cpp:2539-2690
   --bench=N puts WVB2 (mount_ns i64, exec_ns i64, iters i32) before WVO1 and
   WVFO, WVB1 (ns i64, iters i32) before WDBO and WVNO.
 """
@@ -26,8 +32,7 @@ import subprocess
 
 import numpy as np
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-TOOL = os.path.join(ROOT, "welvet.metal_amd", "welvet_dense_fwd")
+TOOL = os.path.join(os.path.dirname(os.path.abspath(__file__)), "welvet_dense_fwd")
 
 
 def run(payload: bytes, *args, timeout=120):
@@ -65,6 +70,19 @@ def wdb(W, x, grad_or_target, use_target, lr, act=-1, dtype=1, bias=None, backen
     out, inn = W.shape
     return (b"WDB1" + _i32(x.shape[0], inn, out, act, dtype, backend) + _f32(W) + _bias(bias) +
             _f32(x) + _i32(int(use_target)) + _f32(grad_or_target) + struct.pack("<d", lr))
+
+
+def wvs(Gate, Up, Down, x, dtype=1, seq=1, backend=0):
+    inter, inn = Gate.shape
+    return (b"WVS1" + _i32(x.shape[0] // seq, seq, inn, inter, dtype, backend) + _f32(Gate) +
+            _f32(Up) + _f32(Down) + _f32(x))
+
+
+def wsb(Gate, Up, Down, x, grad_or_target, use_target, lr, dtype=1, seq=1, backend=0):
+    inter, inn = Gate.shape
+    return (b"WSB1" + _i32(x.shape[0] // seq, seq, inn, inter, dtype, backend) + _f32(Gate) +
+            _f32(Up) + _f32(Down) + _f32(x) + _i32(int(use_target)) + _f32(grad_or_target) +
+            struct.pack("<d", lr))
 
 
 def hops(dims):
@@ -147,6 +165,18 @@ def read_wvo(r: Reader, batch, out):
 
 def read_wdbo(r: Reader):
     assert r.magic() == b"WDBO"
+    res = {k: r.counted() for k in ("pre", "post", "dX", "dW", "W_after")}
+    res["loss"] = r.f64()
+    return res
+
+
+def read_wvso(r: Reader):
+    assert r.magic() == b"WVSO"
+    return r.counted(), r.counted()
+
+
+def read_wsbo(r: Reader):
+    assert r.magic() == b"WSBO"
     res = {k: r.counted() for k in ("pre", "post", "dX", "dW", "W_after")}
     res["loss"] = r.f64()
     return res
