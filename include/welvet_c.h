@@ -79,6 +79,38 @@ WELVET_API welvet_status welvet_swiglu_normalbp_f32(
     const float *grad_or_target, int32_t use_target, double lr, float *pre, float *post, float *dX,
     float *dW, float *W_after, double *loss);
 
+/* reference include/welvet_c.h:184-189 — Sequential Dense chain (the WSQ1
+ * wire): packed [depth][dim][dim] f32, each child a Dense dim -> dim layer
+ * with child_act and no bias, encoded into `dtype`; x [batch*seq*dim] ->
+ * pre = the last child's pre, post = the last child's post. */
+WELVET_API welvet_status welvet_sequential_forward_f32(int32_t batch, int32_t seq, int32_t dim,
+                                                       int32_t depth, int32_t child_act,
+                                                       int32_t dtype, int32_t backend,
+                                                       const float *packed, const float *x,
+                                                       float *pre, float *post);
+/* reference include/welvet_c.h:191-197 — Sequential NormalBP leaf;
+ * dW and W_after [depth][dim][dim]; lr == 0 skips the SGD. */
+WELVET_API welvet_status welvet_sequential_normalbp_f32(
+    int32_t batch, int32_t seq, int32_t dim, int32_t depth, int32_t child_act, int32_t dtype,
+    int32_t backend, const float *packed, const float *x, const float *grad_or_target,
+    int32_t use_target, double lr, float *pre, float *post, float *dX, float *dW, float *W_after,
+    double *loss);
+/* reference include/welvet_c.h:199-203 — Residual y = F(x) + x (the WRE1
+ * wire), F the Dense chain as in welvet_sequential_forward_f32; pre = the
+ * last F child's pre, post = fl32(F(x) + x). */
+WELVET_API welvet_status welvet_residual_forward_f32(int32_t batch, int32_t seq, int32_t dim,
+                                                     int32_t depth, int32_t child_act,
+                                                     int32_t dtype, int32_t backend,
+                                                     const float *packed, const float *x,
+                                                     float *pre, float *post);
+/* reference include/welvet_c.h:205-211 — Residual NormalBP leaf; dX includes
+ * the skip path; dW and W_after are the F children's. */
+WELVET_API welvet_status welvet_residual_normalbp_f32(
+    int32_t batch, int32_t seq, int32_t dim, int32_t depth, int32_t child_act, int32_t dtype,
+    int32_t backend, const float *packed, const float *x, const float *grad_or_target,
+    int32_t use_target, double lr, float *pre, float *post, float *dX, float *dW, float *W_after,
+    double *loss);
+
 /* reference include/welvet_c.h:75-85 — resident session: the packed weights
  * and the [batch] activation buffers stay in HBM; batch is fixed at mount. */
 typedef struct welvet_dense_session welvet_dense_session;

@@ -270,6 +270,55 @@ class Oracle:
                                          for r, sc, sh in parts])
         return res
 
+    # -- Sequential / Residual chains of Dense (src/layers/{sequential,residual}) --
+    def chain_normalbp(self, residual, dtype, packed, x, child_act, grad_or_target=None,
+                       use_target=0, lr=0.0):
+        """welvet_{sequential,residual}_{forward,normalbp}_f32 (c_abi.cpp:918-1090)
+        over sequential.cpp:117-245 / residual.cpp:117-275: packed
+        [depth][dim][dim] Dense children (child_act, no bias) chained on x
+        [rows][dim]; Residual adds fl32(F(x) + x) on the way out and the
+        skip gradient on the way back; SGD children in order (the first error
+        stops).  -> dict(status, pre, post[, dX, dW, W_after, loss])."""
+        packed = np.ascontiguousarray(packed, np.float32)
+        depth, dim = packed.shape[0], packed.shape[1]
+        x = np.ascontiguousarray(x, np.float32)
+        parts, Wd = [], []
+        for i in range(depth):
+            raw, scale = self.pack(dtype, packed[i])
+            parts.append((raw, scale))
+            Wd.append(self.decode_f64(dtype, raw, scale, dim * dim).reshape(dim, dim))
+        ins, pres, cur = [], [], x
+        for i in range(depth):
+            ins.append(cur)
+            p, cur = self.forward(Wd[i], cur, child_act)
+            pres.append(p)
+        post = (cur + x).astype(np.float32) if residual else cur
+        res = dict(status=0, pre=pres[-1], post=post)
+        if grad_or_target is None:
+            return res
+        t = np.ascontiguousarray(grad_or_target, np.float32).reshape(post.shape)
+        loss, gy = 0.0, t
+        if use_target:
+            loss, gy = self.mse(post, t), self.mse_grad(post, t)
+        g, dWs = gy, [None] * depth
+        for i in range(depth - 1, -1, -1):
+            _, g, dWs[i] = self.backward(Wd[i], ins[i], pres[i], g, child_act)
+        res.update(dX=(g + gy).astype(np.float32) if residual else g,
+                   dW=np.concatenate([d.ravel() for d in dWs]), loss=loss)
+        if lr != 0.0:
+            for (raw, scale), dW in zip(parts, dWs):
+                if dtype == 1:
+                    if not np.all(np.isfinite(dW)) or abs(lr) > np.finfo(np.float32).max or \
+                            abs(lr) < np.finfo(np.float32).tiny:
+                        res["status"] = 2
+                        return res
+                    self.sgd_f32(raw.view(np.float32), dW.ravel(), lr)
+                elif self.native_sgd(dtype, raw, scale, dim * dim, dW, lr):
+                    res["status"] = 1
+                    return res
+        res["W_after"] = np.concatenate([self.decode(dtype, r, sc, dim * dim) for r, sc in parts])
+        return res
+
     def forward_native(self, dtype, raw, scale, x, out, inn, act, bias=None, threads=1):
         raw = np.ascontiguousarray(raw, np.uint8)
         x = np.ascontiguousarray(x, np.float32)

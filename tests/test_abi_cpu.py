@@ -88,3 +88,15 @@ def test_swiglu_argument_errors_before_device():
     r = pywelvet.swiglu_normalbp(G, G, D, np.ones((1, 2), np.float32), np.zeros((1, 2)), 1, 0.1,
                                  dtype=-1, status=True)
     assert (r["status"].code, r["status"].message.decode()) == (1, "swiglu nbp: bad dtype -1")
+
+
+@pytest.mark.parametrize("kind", ["sequential", "residual"])
+def test_chain_argument_errors_before_device(kind):
+    """c_abi.cpp:922-928, :956-962, :1017-1023, :1051-1057."""
+    import numpy as np
+    P = np.ones((2, 3, 3), np.float32)
+    st, _, _ = pywelvet.chain_forward(kind, P, np.ones((0, 3), np.float32), status=True)
+    assert (st.code, st.message.decode()) == (1, f"{kind}: invalid argument")
+    r = pywelvet.chain_normalbp(kind, np.ones((0, 3, 3), np.float32), np.ones((1, 3), np.float32),
+                                np.zeros((1, 3)), 1, 0.1, status=True)
+    assert (r["status"].code, r["status"].message.decode()) == (1, f"{kind} nbp: invalid argument")

@@ -439,3 +439,53 @@ def test_swiglu_split_elementwise_closed_form(oracle):
     np.testing.assert_array_equal(d_up, np.zeros(4, np.float32))
     np.testing.assert_array_equal(d_gate, gh * up * np.float32(0.5))
     np.testing.assert_array_equal(oracle.swiglu_h(gate, up), np.zeros(4, np.float32))
+
+
+# ------------------------------------------------ Sequential / Residual chains
+def test_chain_closed_forms(oracle):
+    """Identity children, Linear: Sequential post = x, Residual post = 2x;
+    zero children: Residual post = x, Sequential post = 0; ReLU identity
+    children: Sequential post = relu(x) (Float64 stores hold I exactly)."""
+    rng = np.random.default_rng(31)
+    dim, depth = 8, 3
+    x = rng.normal(0, 1, (4, dim)).astype(np.float32)
+    eye = np.stack([np.eye(dim, dtype=np.float32)] * depth)
+    zero = np.zeros_like(eye)
+    np.testing.assert_array_equal(oracle.chain_normalbp(False, 0, eye, x, -1)["post"], x)
+    np.testing.assert_array_equal(oracle.chain_normalbp(True, 0, eye, x, -1)["post"], 2 * x)
+    np.testing.assert_array_equal(oracle.chain_normalbp(True, 0, zero, x, -1)["post"], x)
+    np.testing.assert_array_equal(oracle.chain_normalbp(False, 0, zero, x, -1)["post"], 0 * x)
+    np.testing.assert_array_equal(oracle.chain_normalbp(False, 0, eye, x, ACT["relu"])["post"],
+                                  np.maximum(x, 0))
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_chain_backward_matches_finite_differences(oracle, residual):
+    """dX and dW (children concatenated in order) against central differences
+    of L = sum(post * g), Float64 weights, tanh children."""
+    rng = np.random.default_rng(32 + residual)
+    dim, depth, rows = 5, 3, 2
+    P = rng.normal(0, 0.6, (depth, dim, dim)).astype(np.float32)
+    x = rng.normal(0, 1, (rows, dim)).astype(np.float32)
+    g = rng.normal(0, 1, (rows, dim)).astype(np.float32)
+    act = ACT["tanh"]
+    r = oracle.chain_normalbp(residual, 0, P, x, act, g, 0, 0.0)
+
+    def L(P_, x_):
+        post = oracle.chain_normalbp(residual, 0, P_, x_, act)["post"].astype(np.float64)
+        return float(np.sum(post * g))
+
+    eps = 1e-2
+    for idx in [(0, 0, 0), (1, 2, 3), (2, dim - 1, 0)]:
+        hi, lo = P.copy(), P.copy()
+        hi[idx] += eps
+        lo[idx] -= eps
+        want = (L(hi, x) - L(lo, x)) / (2 * eps)
+        got = r["dW"][idx[0] * dim * dim + idx[1] * dim + idx[2]]
+        assert abs(got - want) <= 2e-3 * max(1.0, abs(want)), (idx, got, want)
+    for idx in [(0, 0), (1, dim - 1)]:
+        hi, lo = x.copy(), x.copy()
+        hi[idx] += eps
+        lo[idx] -= eps
+        want = (L(P, hi) - L(P, lo)) / (2 * eps)
+        assert abs(r["dX"][idx] - want) <= 2e-3 * max(1.0, abs(want)), (idx, r["dX"][idx], want)

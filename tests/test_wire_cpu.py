@@ -132,3 +132,17 @@ def test_swiglu_wire_parsing():
     full = wire.wsb(G, G, D, x, np.zeros((2, 4)), 1, 0.1)
     rc, out, err = wire.run(full[:-3])  # inside lr: silent exit 2 as the reference
     assert (rc, out, err) == (2, b"", "")
+
+
+def test_chain_wire_parsing():
+    for magic, kind in ((b"WSQ1", "sequential"), (b"WRE1", "residual")):
+        rc, out, err = wire.run(magic + struct.pack("<4i", 1, 1, 4, 2))
+        assert (rc, err.strip()) == (2, "welvet_dense_fwd: short %s header" % magic.decode())
+        rc, out, err = wire.run(magic + struct.pack("<7i", 1, 1, 4, 0, -1, 1, 0))
+        assert (rc, err.strip()) == (2, "welvet_dense_fwd: bad %s dims" % kind)
+        P = np.ones((2, 4, 4), np.float32)
+        rc, out, err = wire.run(wire.chain(magic, P, np.ones((1, 4)))[:-2])
+        assert (rc, out, err) == (2, b"", "")
+    for magic in (b"SQB1", b"REB1"):
+        rc, out, err = wire.run(magic + struct.pack("<2i", 1, 1))
+        assert (rc, err.strip()) == (2, "welvet_dense_fwd: short %s header" % magic.decode())

@@ -10,9 +10,11 @@
 //   WVN1 -> WVNO                      volume NormalBP            volume_fwd.cpp:1759-1929
 //   WVS1 -> WVSO                      SwiGLU forward             main.cpp:650-720
 //   WSB1 -> WSBO                      SwiGLU NormalBP leaf       volume_fwd.cpp:2539-2690
+//   WSQ1 -> WSQO, WRE1 -> WREO        Sequential / Residual      main.cpp:302-430
+//   SQB1 -> SQBO, REB1 -> REBO        their NormalBP leaves      volume_fwd.cpp:6187-6587
 //   --bench=N                         WVB2 (mount_ns, exec_ns, iters) before WVO1 /
-//                                     WVFO; WVB1 (ns, iters) before WDBO / WVNO /
-//                                     WVSO / WSBO
+//                                     WVFO; WVB1 (ns, iters) before every other
+//                                     reply
 //
 // Flags, messages and exit codes follow main.cpp:1253-1711: 2 for a short or
 // malformed wire, 1 for an error the library reports.  Wires of the
@@ -307,6 +309,103 @@ int run_swiglu_normalbp(int bench_iters) {
   return 0;
 }
 
+// ---- WSQ1 / WRE1 / SQB1 / REB1: Sequential and Residual Dense chains ---------
+struct ChainWire {
+  int32_t batch = 0, seq = 0, dim = 0, depth = 0, act = -1, dtype = 1, backend = 0;
+  std::vector<float> packed, x;
+};
+
+// header, packed [depth][dim][dim] and x (main.cpp:302-330, :367-395,
+// volume_fwd.cpp:6187-6208, :6469-6490)
+int read_chain(ChainWire *w, const char *tag, const char *kind, bool check_dims) {
+  if (!read_one(&w->batch) || !read_one(&w->seq) || !read_one(&w->dim) || !read_one(&w->depth) ||
+      !read_one(&w->act) || !read_one(&w->dtype) || !read_one(&w->backend)) {
+    std::fprintf(stderr, "welvet_dense_fwd: short %s header\n", tag);
+    return 2;
+  }
+  if (check_dims && (w->batch <= 0 || w->seq <= 0 || w->dim <= 0 || w->depth <= 0)) {
+    std::fprintf(stderr, "welvet_dense_fwd: bad %s dims\n", kind);
+    return 2;
+  }
+  size_t cn = 0, nw = 0, rows = 0, nx = 0;
+  if (!elems(w->dim, w->dim, &cn) || !elems(w->depth, (int64_t)cn, &nw) ||
+      !elems(w->batch, w->seq, &rows) || !elems((int64_t)rows, w->dim, &nx))
+    return 2;
+  return read_vec(w->packed, nw) && read_vec(w->x, nx) ? 0 : 2;
+}
+
+// WSQ1 -> WSQO, WRE1 -> WREO (main.cpp:302-430): --bench gives WVB1 first
+int run_chain(bool residual, int bench_iters) {
+  ChainWire w;
+  if (int rc = read_chain(&w, residual ? "WRE1" : "WSQ1", residual ? "residual" : "sequential", true))
+    return rc;
+  std::vector<float> pre(w.x.size()), post(w.x.size());
+  auto once = [&]() {
+    auto fn = residual ? welvet_residual_forward_f32 : welvet_sequential_forward_f32;
+    return fn(w.batch, w.seq, w.dim, w.depth, w.act, w.dtype, w.backend, w.packed.data(),
+              w.x.data(), pre.data(), post.data());
+  };
+  if (bench_iters > 0) {
+    for (int i = 0; i < 3; ++i) {
+      welvet_status st = once();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t0 = Clock::now();
+    for (int i = 0; i < bench_iters; ++i) {
+      welvet_status st = once();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t1 = Clock::now();
+    if (!write_exact("WVB1", 4) || !write_one(ns_between(t0, t1)) || !write_one((int32_t)bench_iters))
+      return 2;
+  } else {
+    welvet_status st = once();
+    if (st.code != 0) return fail(st);
+  }
+  return write_exact(residual ? "WREO" : "WSQO", 4) && write_counted(pre) && write_counted(post)
+             ? 0
+             : 2;
+}
+
+// SQB1 -> SQBO, REB1 -> REBO (volume_fwd.cpp:6187-6305, :6469-6587)
+int run_chain_normalbp(bool residual, int bench_iters) {
+  ChainWire w;
+  if (int rc = read_chain(&w, residual ? "REB1" : "SQB1", "", false)) return rc;
+  int32_t use_target = 0;
+  double lr = 0.0;
+  std::vector<float> gyt;
+  if (!read_one(&use_target) || !read_vec(gyt, w.x.size()) || !read_one(&lr)) return 2;
+  std::vector<float> pre(w.x.size()), post(w.x.size()), dX(w.x.size()), dW(w.packed.size()),
+      W_after(w.packed.size());
+  double loss = 0.0;
+  auto step = [&]() {
+    auto fn = residual ? welvet_residual_normalbp_f32 : welvet_sequential_normalbp_f32;
+    return fn(w.batch, w.seq, w.dim, w.depth, w.act, w.dtype, w.backend, w.packed.data(), w.x.data(),
+              gyt.data(), use_target, lr, pre.data(), post.data(), dX.data(), dW.data(),
+              W_after.data(), &loss);
+  };
+  if (bench_iters > 0) {
+    for (int i = 0; i < 3; ++i) {
+      welvet_status st = step();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t0 = Clock::now();
+    for (int i = 0; i < bench_iters; ++i) {
+      welvet_status st = step();
+      if (st.code != 0) return fail(st);
+    }
+    const auto t1 = Clock::now();
+    if (!write_exact("WVB1", 4) || !write_one(ns_between(t0, t1)) || !write_one((int32_t)bench_iters))
+      return 2;
+  }
+  welvet_status st = step();
+  if (st.code != 0) return fail(st);
+  if (!write_exact(residual ? "REBO" : "SQBO", 4) || !write_counted(pre) || !write_counted(post) ||
+      !write_counted(dX) || !write_counted(dW) || !write_counted(W_after) || !write_one(loss))
+    return 2;
+  return 0;
+}
+
 // ---- WVF1 / WVN1: volumes of Dense cells ------------------------------------
 struct GridHeader {
   int32_t depth = 0, rows = 0, cols = 0, lpc = 0, batch = 0, backend = 0, n_links = 0;
@@ -528,20 +627,21 @@ void usage() {
   std::fprintf(stderr,
                "welvet_dense_fwd (welvet.metal_amd, HIP gfx950; Dense wires)\n"
                "  --version | --identity | --gaps | --help\n"
-               "  --bench=N → WVB2 mount_ns+exec_ns (WVD, WVF1) | WVB1 ns (WDB1, WVN1, WVS1, WSB1)\n"
+               "  --bench=N → WVB2 mount_ns+exec_ns (WVD, WVF1) | WVB1 ns (the others)\n"
                "  stdin WVD3/WVD2/WVD1→WVO1 | WVF1→WVFO | WVS1→WVSO (SwiGLU)\n"
-               "       WDB1→WDBO | WVN1→WVNO (Dense NormalBP) | WSB1→WSBO (SwiGLU NormalBP)\n");
+               "       WDB1→WDBO | WVN1→WVNO (Dense NormalBP) | WSB1→WSBO (SwiGLU NormalBP)\n"
+               "       WSQ1→WSQO | WRE1→WREO | SQB1→SQBO | REB1→REBO (Sequential, Residual)\n");
 }
 
 // the reference's wires of other layer kinds (main.cpp:1308-1700): recognised
 // so that a harness sees a clear refusal instead of "bad magic"
 bool other_layer_wire(const char *m) {
   static const char *kOther[] = {
-      "WVM1", "WVR1", "WVL1", "WSM1", "WEM1", "WSQ1", "WRE1", "WSX1", "WVC1", "WVC2",
+      "WVM1", "WVR1", "WVL1", "WSM1", "WEM1", "WSX1", "WVC1", "WVC2",
       "WVC3", "WVT1", "WVT2", "WVT3", "WRN1", "WLS1", "WGD1", "WMB1", "WKM1", "WPL1", "WMC1",
       "WRB1", "WRV1", "WLB1", "WLV1", "WSV1", "WXB1", "WXV1", "WEB1", "WEV1", "WHB1",
       "WHV1", "C1B1", "C2B1", "C3B1", "C1V1", "C2V1", "C3V1", "T1B1", "T2B1", "T3B1", "T1V1",
-      "T2V1", "T3V1", "RNB1", "RNV1", "LSB1", "LSV1", "SQB1", "SQV1", "REB1", "REV1", "MBB1",
+      "T2V1", "T3V1", "RNB1", "RNV1", "LSB1", "LSV1", "SQV1", "REV1", "MBB1",
       "MBV1", "MCB1", "MCV1", "GDB1", "GDV1", "STKB", "STKV", "STB1", "MBP1", "WMV1", "WRF1",
       "WLF1", "WSF1", "WPF1", "WKF1", "WSG1", "SQG1", "REG1", "RNG1", "LSG1", "C1G1", "C2G1",
       "C3G1", "T1G1", "T2G1", "T3G1", "WEG1", "MBG1", "GDG1", "MCG1", "CMB1"};
@@ -597,6 +697,10 @@ int main(int argc, char **argv) {
   if (std::memcmp(magic, "WVN1", 4) == 0) return run_volume_normalbp(bench_iters);
   if (std::memcmp(magic, "WVS1", 4) == 0) return run_swiglu(bench_iters);
   if (std::memcmp(magic, "WSB1", 4) == 0) return run_swiglu_normalbp(bench_iters);
+  if (std::memcmp(magic, "WSQ1", 4) == 0) return run_chain(false, bench_iters);
+  if (std::memcmp(magic, "WRE1", 4) == 0) return run_chain(true, bench_iters);
+  if (std::memcmp(magic, "SQB1", 4) == 0) return run_chain_normalbp(false, bench_iters);
+  if (std::memcmp(magic, "REB1", 4) == 0) return run_chain_normalbp(true, bench_iters);
   const bool v3 = std::memcmp(magic, "WVD3", 4) == 0;
   const bool v2 = std::memcmp(magic, "WVD2", 4) == 0;
   const bool v1 = std::memcmp(magic, "WVD1", 4) == 0;

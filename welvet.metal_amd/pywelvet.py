@@ -84,6 +84,13 @@ def lib() -> C.CDLL:
         L.welvet_swiglu_forward_f32.restype = Status
         L.welvet_swiglu_normalbp_f32.argtypes = sw + [_f, _i32, C.c_double] + [_f] * 5 + [_d]
         L.welvet_swiglu_normalbp_f32.restype = Status
+        ch = [_i32] * 7 + [_f, _f]
+        for nm in ("sequential", "residual"):
+            getattr(L, f"welvet_{nm}_forward_f32").argtypes = ch + [_f, _f]
+            getattr(L, f"welvet_{nm}_forward_f32").restype = Status
+            getattr(L, f"welvet_{nm}_normalbp_f32").argtypes = ch + [_f, _i32, C.c_double] + \
+                [_f] * 5 + [_d]
+            getattr(L, f"welvet_{nm}_normalbp_f32").restype = Status
         L.welvet_hip_volume_train_step_grad.argtypes = [_vp, _f, _i32, _f, _i32, C.c_double, _d,
                                                         _f, _f]
         L.welvet_hip_volume_train_step_grad.restype = Status
@@ -250,6 +257,43 @@ def swiglu_normalbp(Gate, Up, Down, x, grad_or_target, use_target, lr, dtype=1, 
                                           _fp(Down), _fp(x), _fp(g), int(use_target), lr,
                                           _fp(r["pre"]), _fp(r["post"]), _fp(r["dX"]), _fp(r["dW"]),
                                           _fp(r["W_after"]), C.byref(loss))
+    r["loss"] = loss.value
+    if status:
+        r["status"] = st
+        return r
+    check(st)
+    return r
+
+
+def chain_forward(kind, packed, x, child_act=-1, dtype=1, seq=1, status=False):
+    """welvet_{kind}_forward_f32, kind "sequential" or "residual"; packed
+    [depth][dim][dim], x [batch*seq][dim] -> (pre, post)."""
+    packed, x = _f32(packed), _f32(x)
+    depth, dim = packed.shape[0], packed.shape[1]
+    pre = np.zeros(x.shape, np.float32)
+    post = np.zeros(x.shape, np.float32)
+    st = getattr(lib(), f"welvet_{kind}_forward_f32")(x.shape[0] // seq, seq, dim, depth, child_act,
+                                                       dtype, 0, _fp(packed), _fp(x), _fp(pre),
+                                                       _fp(post))
+    if status:
+        return st, pre, post
+    check(st)
+    return pre, post
+
+
+def chain_normalbp(kind, packed, x, grad_or_target, use_target, lr, child_act=-1, dtype=1, seq=1,
+                   status=False):
+    """welvet_{kind}_normalbp_f32 -> dict(pre, post, dX, dW, W_after, loss)."""
+    packed, x, g = _f32(packed), _f32(x), _f32(grad_or_target)
+    depth, dim = packed.shape[0], packed.shape[1]
+    r = dict(pre=np.zeros(x.shape, np.float32), post=np.zeros(x.shape, np.float32),
+             dX=np.zeros(x.shape, np.float32), dW=np.zeros(packed.size, np.float32),
+             W_after=np.zeros(packed.size, np.float32))
+    loss = C.c_double()
+    st = getattr(lib(), f"welvet_{kind}_normalbp_f32")(
+        x.shape[0] // seq, seq, dim, depth, child_act, dtype, 0, _fp(packed), _fp(x), _fp(g),
+        int(use_target), lr, _fp(r["pre"]), _fp(r["post"]), _fp(r["dX"]), _fp(r["dW"]),
+        _fp(r["W_after"]), C.byref(loss))
     r["loss"] = loss.value
     if status:
         r["status"] = st

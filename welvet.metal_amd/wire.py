@@ -23,6 +23,11 @@ build's tool of the same name.
   WSB1      WVS1's fields, then use_target i32; grad_or_target [batch*seq*in];
             lr f64 -> WSBO as WDBO (dW, W_after = concat(Gate, Up, Down))
             tools/dense_fwd/volume_fwd.cpp:2539-2690
+  WSQ1/WRE1 batch, seq, dim, depth, child_act, dtype, backend i32; packed
+            [depth][dim][dim] f32; x [batch*seq*dim]
+            -> WSQO / WREO (n, values) for pre, post   tools/dense_fwd/main.cpp:302-430
+  SQB1/REB1 WSQ1's fields, then use_target i32; grad_or_target; lr f64
+            -> SQBO / REBO as WDBO    tools/dense_fwd/volume_fwd.cpp:6187-6587
   --bench=N puts WVB2 (mount_ns i64, exec_ns i64, iters i32) before WVO1 and
   WVFO, WVB1 (ns i64, iters i32) before WDBO and WVNO.
 """
@@ -83,6 +88,20 @@ def wsb(Gate, Up, Down, x, grad_or_target, use_target, lr, dtype=1, seq=1, backe
     return (b"WSB1" + _i32(x.shape[0] // seq, seq, inn, inter, dtype, backend) + _f32(Gate) +
             _f32(Up) + _f32(Down) + _f32(x) + _i32(int(use_target)) + _f32(grad_or_target) +
             struct.pack("<d", lr))
+
+
+def chain(magic, packed, x, child_act=-1, dtype=1, seq=1, backend=0):
+    """WSQ1 / WRE1 forward wires."""
+    depth, dim = packed.shape[0], packed.shape[1]
+    return (magic + _i32(x.shape[0] // seq, seq, dim, depth, child_act, dtype, backend) +
+            _f32(packed) + _f32(x))
+
+
+def chain_nbp(magic, packed, x, grad_or_target, use_target, lr, child_act=-1, dtype=1, seq=1,
+              backend=0):
+    """SQB1 / REB1 NormalBP wires."""
+    return (chain(magic, packed, x, child_act, dtype, seq, backend) + _i32(int(use_target)) +
+            _f32(grad_or_target) + struct.pack("<d", lr))
 
 
 def hops(dims):
@@ -173,6 +192,20 @@ def read_wdbo(r: Reader):
 def read_wvso(r: Reader):
     assert r.magic() == b"WVSO"
     return r.counted(), r.counted()
+
+
+def read_pair(r: Reader, magic: bytes):
+    """WVSO / WSQO / WREO: counted pre, counted post."""
+    assert r.magic() == magic
+    return r.counted(), r.counted()
+
+
+def read_leaf(r: Reader, magic: bytes):
+    """WDBO-framed NormalBP replies (WSBO, SQBO, REBO)."""
+    assert r.magic() == magic
+    res = {k: r.counted() for k in ("pre", "post", "dX", "dW", "W_after")}
+    res["loss"] = r.f64()
+    return res
 
 
 def read_wsbo(r: Reader):
