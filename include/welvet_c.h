@@ -37,6 +37,43 @@ WELVET_API welvet_status welvet_metal_init(void);
 /* reference include/welvet_c.h:32 — 1 when a gfx950 device is usable */
 WELVET_API int32_t welvet_metal_available(void);
 
+/* reference include/welvet_c.h:35-56 — versioned model sessions (ABI 1):
+ * descriptor WMN1 in, snapshot NWS1 out (reference docs/GO_INTEGRATION.md:
+ * 139-157).  This build mounts Stack and Grid roots whose operations are all
+ * Dense, with every store taken byte for byte from the descriptor's
+ * snapshots; other roots, layer kinds, credit families and CamSync answer
+ * code 2.  Inputs are copied during the call; blobs are freed with
+ * welvet_metal_blob_free. */
+typedef struct welvet_model_session welvet_model_session;
+typedef struct welvet_metal_blob {
+  uint8_t *data;
+  size_t size;
+} welvet_metal_blob;
+WELVET_API int32_t welvet_model_abi_version(void);
+WELVET_API welvet_status welvet_model_mount(const uint8_t *descriptor, size_t size,
+                                            welvet_model_session **out);
+WELVET_API welvet_status welvet_model_forward(welvet_model_session *s, const uint8_t *input,
+                                              size_t size, welvet_metal_blob *out);
+WELVET_API welvet_status welvet_model_train_credit(welvet_model_session *s, int32_t mode,
+                                                   double lr, const uint8_t *data, size_t size);
+WELVET_API welvet_status welvet_model_dense_proxy(welvet_model_session *s, int32_t kind,
+                                                  const uint8_t *data, size_t size,
+                                                  welvet_metal_blob *out);
+WELVET_API welvet_status welvet_model_forward_pair(welvet_model_session *s, const uint8_t *data,
+                                                   size_t size, welvet_metal_blob *out);
+WELVET_API welvet_status welvet_model_backward(welvet_model_session *s, const uint8_t *data,
+                                               size_t size, welvet_metal_blob *out);
+WELVET_API welvet_status welvet_model_apply_sgd(welvet_model_session *s, double lr,
+                                                const uint8_t *data, size_t size);
+WELVET_API welvet_status welvet_model_train_mse(welvet_model_session *s, int32_t mode, double lr,
+                                                int32_t ticks, const uint8_t *data, size_t size,
+                                                double *loss);
+WELVET_API welvet_status welvet_model_export_weights(welvet_model_session *s,
+                                                     welvet_metal_blob *out);
+WELVET_API welvet_status welvet_model_sync(welvet_model_session *s, int32_t event);
+WELVET_API void welvet_model_release(welvet_model_session *s);
+WELVET_API void welvet_metal_blob_free(welvet_metal_blob *b);
+
 /* reference include/welvet_c.h:59-62 — one-shot mount + execute + release.
  * W_init [out*in] row-major f32, encoded into `dtype` (0..33); bias [bias_len]
  * f64 (nullable) added for o < bias_len; x [batch*in]; pre/post [batch*out].

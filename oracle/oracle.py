@@ -390,6 +390,83 @@ def have_reference() -> bool:
     return os.path.exists(REF_SO)
 
 
+class Stack:
+    """CPU restatement of a Stack of Dense children (the model ABI's root 0).
+
+    TEST INFRASTRUCTURE ONLY.  stack::forward / backward_f32 / apply_grad_sgd
+    (src/layers/stack/stack.cpp:446-556) over Dense children in order, and
+    cameral_train::train_stack_mse for the back-propagation family
+    (src/runtime/cameral_train.cpp:348-403: forward, MSE, backward, SGD of
+    every child in order even at lr 0).  Each child holds its packed store
+    (raw, scale) like Volume's cells."""
+
+    def __init__(self, oracle: Oracle):
+        self.O = oracle
+        self.children = []
+
+    def add_dense(self, W, act=-1, dtype=1, bias=None):
+        W = np.ascontiguousarray(W, np.float32)
+        raw, scale = self.O.pack(dtype, W)
+        self.children.append(dict(dtype=dtype, act=act, raw=raw, scale=scale, out=W.shape[0],
+                                  inn=W.shape[1],
+                                  bias=None if bias is None else np.asarray(bias, np.float64)))
+
+    def _wd(self, c):
+        return self.O.decode_f64(c["dtype"], c["raw"], c["scale"],
+                                 c["out"] * c["inn"]).reshape(c["out"], c["inn"])
+
+    def export_f32(self, i):
+        c = self.children[i]
+        return self.O.decode(c["dtype"], c["raw"], c["scale"], c["out"] * c["inn"]).reshape(
+            c["out"], c["inn"])
+
+    def forward(self, x):
+        """-> (ins, pres, posts)."""
+        cur = np.ascontiguousarray(x, np.float32)
+        ins, pres, posts = [], [], []
+        for c in self.children:
+            ins.append(cur)
+            p, cur = self.O.forward(self._wd(c), cur, c["act"], c["bias"])
+            pres.append(p)
+            posts.append(cur)
+        return ins, pres, posts
+
+    def backward(self, x, gy):
+        """-> (gx, dW concatenated in child order)."""
+        ins, pres, _ = self.forward(x)
+        g = np.ascontiguousarray(gy, np.float32)
+        dws = [None] * len(self.children)
+        for i in range(len(self.children) - 1, -1, -1):
+            c = self.children[i]
+            _, g, dws[i] = self.O.backward(self._wd(c), ins[i], pres[i], g, c["act"])
+        return g, np.concatenate([d.ravel() for d in dws])
+
+    def apply_sgd(self, dw, lr):
+        """-> status code (0, or the first failing child's)."""
+        off = 0
+        for c in self.children:
+            n = c["out"] * c["inn"]
+            g = np.ascontiguousarray(dw[off:off + n], np.float32)
+            off += n
+            if c["dtype"] == 1:
+                if not np.all(np.isfinite(g)) or abs(lr) > np.finfo(np.float32).max or \
+                        (lr != 0 and abs(lr) < np.finfo(np.float32).tiny):
+                    return 2
+                self.O.sgd_f32(c["raw"].view(np.float32), g, lr)
+            elif self.O.native_sgd(c["dtype"], c["raw"], c["scale"], n, g, lr):
+                return 1
+        return 0
+
+    def train_mse(self, x, t, lr, frozen=False):
+        """-> (status, loss)."""
+        _, _, posts = self.forward(x)
+        loss = self.O.mse(posts[-1], t)
+        if frozen:
+            return 0, loss
+        gx, dw = self.backward(x, self.O.mse_grad(posts[-1], t))
+        return self.apply_sgd(dw, lr), loss
+
+
 class Volume:
     """CPU restatement of the volume runtime over Dense cells.
 

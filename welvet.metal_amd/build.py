@@ -25,7 +25,7 @@ LIB = os.path.join(HERE, "libwelvet_hip.so")
 TOOL = os.path.join(HERE, "welvet_dense_fwd")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 CXX = os.environ.get("CXX", "g++")
-SOURCES = ["codec.hip", "dense.hip", "runtime.cpp", "volume.cpp", "swiglu.cpp", "chain.cpp"]
+SOURCES = ["codec.hip", "dense.hip", "runtime.cpp", "volume.cpp", "swiglu.cpp", "chain.cpp", "model.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -18,8 +18,10 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/welvet_c.h"
+#include "codec.hpp"
 #include "runtime.hpp"
 
 using namespace wh;
@@ -176,6 +178,61 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
     WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
     WH_HIP(hipStreamSynchronize(s));
   }
+  return ok();
+}
+
+welvet_status store_from_native(Store *w, int dtype, int rows, int cols, float scale,
+                                const float *f32, size_t nf32, const uint8_t *raw, size_t nraw,
+                                hipStream_t s) {
+  if (dtype < 0 || dtype >= kNumDTypes || !dims_ok(rows, cols) || !std::isfinite(scale))
+    return make_status(kInvalid, "native store metadata mismatch");
+  const int64_t n = (int64_t)rows * cols;
+  const bool is_f32 = dtype == kFloat32;
+  if (is_f32 ? (nf32 != (size_t)n || nraw != 0) : (nf32 != 0 || nraw != (size_t)native_bytes(dtype, n)))
+    return make_status(kInvalid, "native store payload length mismatch");
+  w->dtype = dtype;
+  w->rows = rows;
+  w->cols = cols;
+  w->body_bytes = (size_t)((n * dtype_bits(dtype) + 7) / 8);
+  const size_t alloc = ((w->body_bytes + 64 + 255) / 256) * 256;
+  WH_HIP(hipMalloc(&w->body, alloc));
+  WH_HIP(hipMemsetAsync(w->body, 0, alloc, s));
+  if (is_f32) {  // WeightStore::f32; the scale of a Float32 store is 1 (encode_format_none)
+    WH_HIP(hipMemcpyAsync(w->body, f32, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    w->scale = 1.0f;
+    w->minv = 0.0f;
+    WH_HIP(hipStreamSynchronize(s));
+    return ok();
+  }
+  const size_t hdr = dtype_has_min(dtype) ? 4 : 0;
+  w->scale = scale;
+  w->minv = 0.0f;
+  if (hdr) std::memcpy(&w->minv, raw, 4);
+  WH_HIP(hipMemcpyAsync(w->body, raw + hdr, w->body_bytes, hipMemcpyHostToDevice, s));
+  std::vector<uint8_t> k;
+  if (dtype == kFP8E4M3 || dtype == kFP8E5M2) {  // the decode-ready copy, made on the host
+    k.resize(w->body_bytes);
+    bool finite = true;
+    for (size_t i = 0; i < k.size(); ++i) {
+      const uint32_t c = raw[hdr + i];
+      if (dtype == kFP8E4M3) {
+        k[i] = kcode<kFP8E4M3>(c);
+      } else {
+        k[i] = kcode<kFP8E5M2>(c);
+        finite = finite && (c & 0x7cu) != 0x7cu;
+      }
+    }
+    w->finite = finite;
+    WH_HIP(hipMalloc(&w->kbody, alloc));
+    WH_HIP(hipMemsetAsync(w->kbody, 0, alloc, s));
+    WH_HIP(hipMemcpyAsync(w->kbody, k.data(), k.size(), hipMemcpyHostToDevice, s));
+  }
+  if (dtype_lut(dtype)) {
+    WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
+    WH_HIP(launch_lut(dtype, w->scale, w->minv, w->lut, s));
+    WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
+  }
+  WH_HIP(hipStreamSynchronize(s));  // k and the caller's buffers outlive the copies
   return ok();
 }
 

@@ -62,6 +62,12 @@ welvet_status store_prepare_backward(Store *w, int batch, hipStream_t s);
 // WeightStore::make on the device from f32 values already in HBM.
 welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d_w, hipStream_t s);
 welvet_status store_set_bias(Store *w, const double *bias, size_t bias_len, hipStream_t s);
+// A store from the fields of a WeightStore snapshot (model_session.cpp:128-151
+// read_store): Float32 takes the f32 payload, the other dtypes the native
+// bytes in the reference layout (4-byte min header for the unsigned types).
+welvet_status store_from_native(Store *w, int dtype, int rows, int cols, float scale,
+                                const float *f32, size_t nf32, const uint8_t *raw, size_t nraw,
+                                hipStream_t s);
 welvet_status store_from_host(Store *w, int dtype, int rows, int cols, const float *W_init,
                               hipStream_t s);
 // WeightStore::apply_sgd with a device gradient; synchronises to check it.
@@ -69,6 +75,18 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
 welvet_status store_native(const Store &w, uint8_t *out, size_t cap, size_t *len, hipStream_t s);
 welvet_status store_export(const Store &w, float *d_out, hipStream_t s);
 bool dims_ok(int32_t rows, int32_t cols);
+
+// Volume hooks for the model sessions (volume.cpp): bind a ready store (taken
+// over), read a bound cell's store, change the batch, and
+// cameral_train::train_volume_mse of the BP family (forward, MSE loss, then
+// backward and SGD unless `frozen` or lr == 0).
+welvet_status grid_bind_store(welvet_hip_grid *g, int z, int y, int x, int l, int in, int out,
+                              int act, Store *W);
+const Store *grid_store(welvet_hip_grid *g, int z, int y, int x, int l);
+int grid_batch(const welvet_hip_grid *g);
+welvet_status grid_set_batch(welvet_hip_grid *g, int batch);
+welvet_status grid_train_volume_mse(welvet_hip_grid *g, const float *x, int in, const float *target,
+                                    int out, double lr, bool frozen, double *loss);
 
 }  // namespace rt
 }  // namespace wh

@@ -179,10 +179,17 @@ const float *tape_output(const Grid *g) { return g->cells[g->tape.back()].post; 
 // host reads the first code once, at the end.  grad_in (host, nullable)
 // receives backward::Result::grad_in, the first entry's input gradient.
 welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr, double *loss,
-                       float *grad_in, hipStream_t s) {
+                       float *grad_in, hipStream_t s, bool loss_only = false) {
   const int64_t ny = (int64_t)g->batch * out_width;
   WH_HIP(hipMemsetAsync(g->d_flag, 0, (2 + g->tape.size()) * sizeof(int), s));
   WH_HIP(launch_mse(tape_output(g), d_target, ny, g->d_loss, g->d_gy, g->ws, g->ws_bytes, s));
+  if (loss_only) {
+    double h_loss = 0.0;
+    WH_HIP(hipMemcpyAsync(&h_loss, g->d_loss, sizeof(double), hipMemcpyDeviceToHost, s));
+    WH_HIP(hipStreamSynchronize(s));
+    if (loss) *loss = h_loss;
+    return ok();
+  }
   // the gradient a step passes back must fit the step before it in the tape
   // (a remote hop can break the chain: dense::backward_f32 dense.cpp:171-178)
   for (size_t i = g->tape.size() - 1; i > 0; --i) {
@@ -274,6 +281,48 @@ welvet_status prepare_step(Grid *g, int out_width) {
   return grow(&g->dpre, &g->dpre_elems, g->batch * max_out);
 }
 
+// bind_dense's work after its checks: the cell's store is *W (taken over)
+// when W is given, else W_init encoded into dtype with the bias; then the
+// cell's pre/post buffers and the forward workspace.
+welvet_status bind_cell(Grid *g, int z, int y, int x, int l, int in, int out, int act, Store *W,
+                        int dtype, const float *W_init, const double *bias, size_t bias_len) {
+  Grid::Cell &c = g->cells[cell_index(*g, z, y, x, l)];
+  WH_HIP(hipStreamSynchronize(g->stream));
+  const bool remote = c.remote, disabled = c.disabled;
+  const int tz = c.tz, ty = c.ty, tx = c.tx, tl = c.tl;
+  free_cell(&c);
+  c = Grid::Cell();
+  c.remote = remote;
+  c.disabled = disabled;
+  c.tz = tz, c.ty = ty, c.tx = tx, c.tl = tl;
+  c.in = in;
+  c.out = out;
+  c.act = act;
+  welvet_status st = ok();
+  if (W != nullptr) {  // take the store over
+    c.W = *W;
+    *W = Store();
+  } else {
+    st = store_from_host(&c.W, dtype, out, in, W_init, g->stream);
+    if (st.code == 0) st = store_set_bias(&c.W, bias, bias_len, g->stream);
+  }
+  if (st.code == 0) {
+    const size_t yb = (size_t)g->batch * out * sizeof(float);
+    hipError_t e = hipMalloc(&c.pre, yb);
+    if (e == hipSuccess) e = hipMalloc(&c.post, yb);
+    if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
+    if (e != hipSuccess) st = make_status(kInternal, "hip: %s", hipGetErrorString(e));
+  }
+  if (st.code == 0) st = grow_ws(g, forward_workspace_bytes(c.W.dev(), g->batch));
+  if (st.code) {
+    free_cell(&c);
+    return st;
+  }
+  c.bound = true;
+  g->tape.clear();
+  return ok();
+}
+
 welvet_status cell_at(Grid *g, int z, int y, int x, int l, Grid::Cell **c) {
   if (!in_grid(*g, z, y, x, l)) return bad_coord("cell", z, y, x, l);
   *c = &g->cells[cell_index(*g, z, y, x, l)];
@@ -337,36 +386,74 @@ welvet_status welvet_hip_grid_bind_dense(welvet_hip_grid *g, int32_t z, int32_t 
   if (dtype < 0 || dtype >= kNumDTypes)
     return make_status(kUnsupported, "dense HIP unsupported dtype %d", dtype);
   if (!dims_ok(out, in)) return make_status(kInvalid, "weights: bad shape");
-  Grid::Cell &c = g->cells[cell_index(*g, z, y, x, l)];
+  return bind_cell(g, z, y, x, l, in, out, act, nullptr, dtype, W_init, bias, bias_len);
+}
+
+}  // extern "C"
+
+namespace wh {
+namespace rt {
+
+welvet_status grid_bind_store(welvet_hip_grid *g, int z, int y, int x, int l, int in, int out,
+                              int act, Store *W) {
+  std::lock_guard<std::mutex> lk(g->mu);
+  if (!in_grid(*g, z, y, x, l)) return bad_coord("bind", z, y, x, l);
+  return bind_cell(g, z, y, x, l, in, out, act, W, 0, nullptr, nullptr, 0);
+}
+
+const Store *grid_store(welvet_hip_grid *g, int z, int y, int x, int l) {
+  if (!g || !in_grid(*g, z, y, x, l)) return nullptr;
+  const Grid::Cell &c = g->cells[cell_index(*g, z, y, x, l)];
+  return c.bound ? &c.W : nullptr;
+}
+
+welvet_status grid_train_volume_mse(welvet_hip_grid *g, const float *x, int in, const float *target,
+                                    int out, double lr, bool frozen, double *loss) {
+  if (!g || !loss) return make_status(kInvalid, "cameral volume arguments");
+  if (!x || in <= 0) return make_status(kInvalid, "runtime.forward: empty input");
+  std::lock_guard<std::mutex> lk(g->mu);
+  welvet_status st = grow(&g->d_x, &g->x_elems, (int64_t)g->batch * in);
+  if (st.code) return st;
+  int out_w = 0;
+  st = plan_forward(g, g->d_x, in, &out_w);
+  if (st.code) return st;
+  if (!target || out != out_w) return make_status(kInvalid, "training: MSE shape");
+  st = grow(&g->d_t, &g->t_elems, (int64_t)g->batch * out);
+  if (st.code == 0) st = prepare_step(g, out);
+  if (st.code) return st;
+  WH_HIP(hipMemcpyAsync(g->d_x, x, (size_t)g->batch * in * sizeof(float), hipMemcpyHostToDevice,
+                        g->stream));
+  WH_HIP(hipMemcpyAsync(g->d_t, target, (size_t)g->batch * out * sizeof(float),
+                        hipMemcpyHostToDevice, g->stream));
+  st = run_forward(g, g->stream);
+  if (st.code) return st;
+  return run_step(g, g->d_t, out, lr, loss, nullptr, g->stream, frozen || lr == 0.0);
+}
+
+int grid_batch(const welvet_hip_grid *g) { return g->batch; }
+
+welvet_status grid_set_batch(welvet_hip_grid *g, int batch) {
+  if (batch <= 0) return make_status(kInvalid, "bad resident dims");
+  std::lock_guard<std::mutex> lk(g->mu);
+  if (batch == g->batch) return ok();
   WH_HIP(hipStreamSynchronize(g->stream));
-  const bool remote = c.remote, disabled = c.disabled;
-  const int tz = c.tz, ty = c.ty, tx = c.tx, tl = c.tl;
-  free_cell(&c);
-  c = Grid::Cell();
-  c.remote = remote;
-  c.disabled = disabled;
-  c.tz = tz, c.ty = ty, c.tx = tx, c.tl = tl;
-  c.in = in;
-  c.out = out;
-  c.act = act;
-  welvet_status st = store_from_host(&c.W, dtype, out, in, W_init, g->stream);
-  if (st.code == 0) st = store_set_bias(&c.W, bias, bias_len, g->stream);
-  if (st.code == 0) {
-    const size_t yb = (size_t)g->batch * out * sizeof(float);
-    hipError_t e = hipMalloc(&c.pre, yb);
-    if (e == hipSuccess) e = hipMalloc(&c.post, yb);
-    if (e == hipSuccess) e = hipStreamSynchronize(g->stream);
-    if (e != hipSuccess) st = make_status(kInternal, "hip: %s", hipGetErrorString(e));
+  for (Grid::Cell &c : g->cells) {
+    if (!c.bound) continue;
+    for (float **p : {&c.pre, &c.post}) {
+      if (*p) WH_HIP(hipFree(*p));
+      *p = nullptr;
+      WH_HIP(hipMalloc(p, (size_t)batch * c.out * sizeof(float)));
+    }
   }
-  if (st.code == 0) st = grow_ws(g, forward_workspace_bytes(c.W.dev(), g->batch));
-  if (st.code) {
-    free_cell(&c);
-    return st;
-  }
-  c.bound = true;
+  g->batch = batch;  // the step buffers regrow on demand
   g->tape.clear();
   return ok();
 }
+
+}  // namespace rt
+}  // namespace wh
+
+extern "C" {
 
 welvet_status welvet_hip_grid_set_remote_link(welvet_hip_grid *g, int32_t z, int32_t y, int32_t x,
                                               int32_t l, int32_t tz, int32_t ty, int32_t tx,

@@ -48,6 +48,11 @@ class WelvetError(RuntimeError):
 _f = C.POINTER(C.c_float)
 _d = C.POINTER(C.c_double)
 _u8 = C.POINTER(C.c_uint8)
+
+
+class Blob(C.Structure):
+    """welvet_metal_blob: a library-owned byte buffer."""
+    _fields_ = [("data", C.POINTER(C.c_uint8)), ("size", C.c_size_t)]
 _vp = C.c_void_p
 _i32 = C.c_int32
 
@@ -91,6 +96,26 @@ def lib() -> C.CDLL:
             getattr(L, f"welvet_{nm}_normalbp_f32").argtypes = ch + [_f, _i32, C.c_double] + \
                 [_f] * 5 + [_d]
             getattr(L, f"welvet_{nm}_normalbp_f32").restype = Status
+        _bp = C.POINTER(Blob)
+        L.welvet_model_abi_version.argtypes = []
+        L.welvet_model_abi_version.restype = _i32
+        L.welvet_model_mount.argtypes = [_u8, C.c_size_t, C.POINTER(_vp)]
+        L.welvet_model_mount.restype = Status
+        for nm in ("forward", "forward_pair", "backward"):
+            getattr(L, f"welvet_model_{nm}").argtypes = [_vp, _u8, C.c_size_t, _bp]
+            getattr(L, f"welvet_model_{nm}").restype = Status
+        L.welvet_model_apply_sgd.argtypes = [_vp, C.c_double, _u8, C.c_size_t]
+        L.welvet_model_apply_sgd.restype = Status
+        L.welvet_model_train_mse.argtypes = [_vp, _i32, C.c_double, _i32, _u8, C.c_size_t, _d]
+        L.welvet_model_train_mse.restype = Status
+        L.welvet_model_export_weights.argtypes = [_vp, _bp]
+        L.welvet_model_export_weights.restype = Status
+        L.welvet_model_sync.argtypes = [_vp, _i32]
+        L.welvet_model_sync.restype = Status
+        L.welvet_model_release.argtypes = [_vp]
+        L.welvet_model_release.restype = None
+        L.welvet_metal_blob_free.argtypes = [_bp]
+        L.welvet_metal_blob_free.restype = None
         L.welvet_hip_volume_train_step_grad.argtypes = [_vp, _f, _i32, _f, _i32, C.c_double, _d,
                                                         _f, _f]
         L.welvet_hip_volume_train_step_grad.restype = Status
@@ -300,6 +325,60 @@ def chain_normalbp(kind, packed, x, grad_or_target, use_target, lr, child_act=-1
         return r
     check(st)
     return r
+
+
+class Model:
+    """welvet_model_* session (ABI 1): mount a WMN1 descriptor; calls take and
+    return the ABI's byte messages."""
+
+    def __init__(self, descriptor: bytes, status=False):
+        self.h = C.c_void_p()
+        buf = (C.c_uint8 * max(1, len(descriptor))).from_buffer_copy(descriptor or b"\0")
+        self.status = lib().welvet_model_mount(buf, len(descriptor), C.byref(self.h))
+        if not status:
+            check(self.status)
+
+    @staticmethod
+    def _buf(b: bytes):
+        return (C.c_uint8 * max(1, len(b))).from_buffer_copy(b or b"\0")
+
+    def _blob_call(self, fn, *args):
+        blob = Blob()
+        st = fn(self.h, *args, C.byref(blob))
+        data = bytes(C.string_at(blob.data, blob.size)) if st.code == 0 and blob.size else b""
+        lib().welvet_metal_blob_free(C.byref(blob))
+        return st, data
+
+    def call(self, name: str, payload: bytes):
+        """forward / forward_pair / backward -> (status, reply bytes)."""
+        return self._blob_call(getattr(lib(), f"welvet_model_{name}"), self._buf(payload),
+                               len(payload))
+
+    def train_mse(self, mode: int, lr: float, payload: bytes, ticks: int = 1):
+        loss = C.c_double()
+        st = lib().welvet_model_train_mse(self.h, mode, lr, ticks, self._buf(payload), len(payload),
+                                          C.byref(loss))
+        return st, loss.value
+
+    def apply_sgd(self, lr: float, payload: bytes):
+        return lib().welvet_model_apply_sgd(self.h, lr, self._buf(payload), len(payload))
+
+    def export(self):
+        return self._blob_call(lib().welvet_model_export_weights)
+
+    def sync(self, event: int):
+        return lib().welvet_model_sync(self.h, event)
+
+    def close(self):
+        if self.h:
+            lib().welvet_model_release(self.h)
+            self.h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 class Session:

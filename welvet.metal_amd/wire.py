@@ -230,3 +230,79 @@ def read_wvno(r: Reader):
     res["W_after"] = cells
     res["y"] = r.counted()
     return res
+
+
+# ---- model sessions: WMN1 descriptors, tensors, NWS1 snapshots ---------------
+# src/interop/model_session.cpp:99-160, :319-404, :521-550;
+# include/welvet/interop/child_wire.hpp:21-55 (Dense child);
+# include/welvet/interop/model_wire.hpp:195-263 (Cameral controls).
+
+def plain_controls():
+    """Controls with no modes, no branch rates, zero coefficients, no CamSync."""
+    return _i32(0) + _i32(0) + struct.pack("<3d", 0.0, 0.0, 0.0) + _i32(0)
+
+
+def dense_child(W, act=-1, dtype=1, bias=None):
+    out, inn = W.shape
+    return _i32(1, inn, out, act, dtype) + _f32(W) + _bias(bias)
+
+
+def store_snapshot(dtype, rows, cols, scale, f32=None, raw=None, bias=None):
+    """One WeightStore record: dtype, rows, cols, scale, counted f32, counted
+    native bytes, counted f64 bias."""
+    f = np.zeros(0, np.float32) if f32 is None else np.ascontiguousarray(f32, np.float32).ravel()
+    r = np.zeros(0, np.uint8) if raw is None else np.ascontiguousarray(raw, np.uint8).ravel()
+    b = np.zeros(0, np.float64) if bias is None else np.ascontiguousarray(bias, np.float64)
+    return (_i32(dtype, rows, cols) + struct.pack("<f", scale) + _i32(f.size) + f.tobytes() +
+            _i32(r.size) + r.tobytes() + _i32(b.size) + b.tobytes())
+
+
+def wmn1(root, children, snapshots, dims=(1, 1, 1, 1), cells=None):
+    """children: list of child records (bytes; b"" + _i32(0) for an empty
+    one), snapshots: the store records in child order, cells (Grid root):
+    per cell (enabled, remote, tz, ty, tx, tl)."""
+    b = struct.pack("<I", 0x314E4D57) + _i32(root, len(children), *dims)
+    for c in children:
+        b += c
+    b += plain_controls()
+    for _ in children:
+        b += plain_controls()
+    b += _i32(len(snapshots))
+    for sn in snapshots:
+        b += sn
+    for meta in cells or ():
+        b += _i32(*meta)
+    return b
+
+
+def empty_child():
+    return _i32(0)
+
+
+def tensor(a):
+    a = np.ascontiguousarray(a, np.float32)
+    return _i32(a.ndim, *a.shape) + a.tobytes()
+
+
+def read_tensor(r: Reader):
+    shape = tuple(r.i32() for _ in range(r.i32()))
+    return r.counted().reshape(shape)
+
+
+def read_nws1(data: bytes):
+    """-> list of dict(dtype, rows, cols, scale, f32, raw, bias) and the
+    count of extra (Mamba/GDN) records."""
+    r = Reader(data)
+    assert r.take(4) == struct.pack("<I", 0x3153574E)
+    stores = []
+    for _ in range(r.i32()):
+        dt, rows, cols = r.i32(), r.i32(), r.i32()
+        scale = struct.unpack("<f", r.take(4))[0]
+        f = r.counted()
+        raw = np.frombuffer(r.take(r.i32()), np.uint8).copy()
+        bias = np.frombuffer(r.take(8 * r.i32()), np.float64).copy()
+        stores.append(dict(dtype=dt, rows=rows, cols=cols, scale=scale, f32=f, raw=raw, bias=bias))
+    extras = r.i32()
+    assert r.done()
+    return stores, extras
+
