@@ -203,6 +203,45 @@ def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, ini
             "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def time_swiglu_forward(torch, P, inn, inter, dtype, batch, steps, warmup, seed):
+    """Resident SwiGLU forward (Gate and Up GEMVs/GEMMs, op_swiglu, Down) on
+    device buffers; rotates mounted copies so the working set exceeds the
+    MALL."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    wbytes = 3 * inn * inter * P.dtype_bits(dtype) // 8
+    copies = max(2, -(-MALL_BYTES // wbytes))
+    G, U, D = (_weights(rng, *shape, "normal") for shape in ((inter, inn), (inter, inn), (inn, inter)))
+    layers = [P.SwigluSession(G, U, D, batch, dtype) for _ in range(copies)]
+    del G, U, D
+    dev = torch.device("cuda:0")
+    x = torch.randn((batch, inn), device=dev)
+    h = torch.empty((batch, inter), device=dev)
+    y = torch.empty((batch, inn), device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    sh = stream.cuda_stream
+
+    def step(i):
+        P.check(layers[i % copies].forward_device(x.data_ptr(), h.data_ptr(), y.data_ptr(), sh))
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    for L in layers:
+        L.close()
+    flops = 2.0 * batch * 3 * inn * inter
+    return {"shape": [inn, inter], "weight_dtype": P.DTYPE_NAMES[dtype], "batch": batch,
+            "packed_bytes": wbytes, "weight_copies": copies, "ms_per_step": ms,
+            "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
+
+
 def time_volume_train(torch, P, dims, widths, dtype, batch, steps, seed, lr=1e-3):
     """training::step_dense on device buffers (forward, MSE vs N(0,1) targets,
     backward, SGD with re-encode); one synchronisation per step."""
@@ -268,6 +307,10 @@ def run_configs(torch, P, only=("c2", "c3", "c4", "c5")):
         for b in (1, 8, 64):
             out[f"c3_{name}_4096-11008-4096_b{b}"] = time_volume_forward(
                 torch, P, [4096, 11008, 4096], dt, b, 50, 5, seed + 2, init=init)
+    for name, dt in (("nf4", 26), ("fp4", 16)) if "c3" in only else ():
+        for b in (1, 8, 64):  # the config-3 shape as one SwiGLU (Gate, Up, Down)
+            out[f"c3_swiglu_{name}_4096x11008_b{b}"] = time_swiglu_forward(
+                torch, P, 4096, 11008, dt, b, 50, 5, seed + 5)
     for name, dt in (("int8", 9), ("e4m3", 4)) if "c4" in only else ():
         out[f"c4_{name}_2048-8192-2048_b256"] = time_volume_train(
             torch, P, (1, 1, 2, 1), [2048, 8192, 2048], dt, 256, 10, seed + 3)

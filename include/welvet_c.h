@@ -253,6 +253,21 @@ WELVET_API welvet_status welvet_hip_grid_native(welvet_hip_grid *g, int32_t z, i
                                                 int32_t x, int32_t l, uint8_t *out, size_t cap,
                                                 size_t *len, float *scale);
 
+/* Resident SwiGLU: welvet_swiglu_forward_f32's layer kept mounted (the
+ * three stores packed in HBM, `rows` = batch * seq fixed at mount), its
+ * forward on device pointers (16-byte aligned) enqueued on `stream`:
+ * x [rows*in] -> pre = h [rows*inter], post [rows*in].  Calls on one handle
+ * must not overlap (they share its intermediate buffers). */
+typedef struct welvet_hip_swiglu welvet_hip_swiglu;
+WELVET_API welvet_status welvet_hip_swiglu_mount(int32_t rows, int32_t input_dim,
+                                                 int32_t intermediate_dim, int32_t dtype,
+                                                 const float *Gate, const float *Up,
+                                                 const float *Down, welvet_hip_swiglu **s);
+WELVET_API welvet_status welvet_hip_swiglu_forward_device(welvet_hip_swiglu *s, const float *d_x,
+                                                          float *d_pre, float *d_post,
+                                                          void *stream);
+WELVET_API void welvet_hip_swiglu_release(welvet_hip_swiglu *s);
+
 /* Kernel route of the forward: 0 auto, 1 GEMV, 2 MFMA GEMM, 3 element-wise. */
 WELVET_API void welvet_hip_set_forward_path(int32_t path);
 /* Kernel tuning knob `key` := value, returns the previous value (-1 = unknown

@@ -139,3 +139,37 @@ def test_c3_shape_forward(oracle):
             o = oracle.swiglu_normalbp(dtype, G, U, D, x)
             assert rel_err(pre, o["pre"]) <= 1e-5
             assert rel_err(post, o["post"]) <= 1e-4  # K = 11008 in Down: the 1e-4 bar
+
+
+def test_resident_session_matches_one_shot():
+    """welvet_hip_swiglu_forward_device gives the one-shot forward's bytes
+    (device buffers from the HIP runtime the library itself uses)."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipFree.argtypes = [C.c_void_p]
+    rng = np.random.default_rng(501)
+    inn, inter, rows = 256, 688, 8
+    G, U, D = _weights(rng, inter, inn, 26)
+    x = rng.normal(0, 1, (rows, inn)).astype(np.float32)
+    pre, post = pywelvet.swiglu_forward(G, U, D, x, dtype=26)
+    bufs = []
+    for n in (x.nbytes, pre.nbytes, post.nbytes):
+        p = C.c_void_p()
+        assert hip.hipMalloc(C.byref(p), n) == 0
+        bufs.append(p)
+    try:
+        assert hip.hipMemcpy(bufs[0], x.ctypes.data, x.nbytes, 1) == 0  # host to device
+        with pywelvet.SwigluSession(G, U, D, rows, dtype=26) as L:
+            for _ in range(2):
+                pywelvet.check(L.forward_device(bufs[0].value, bufs[1].value, bufs[2].value))
+            assert hip.hipDeviceSynchronize() == 0
+        h, y = np.empty_like(pre), np.empty_like(post)
+        assert hip.hipMemcpy(h.ctypes.data, bufs[1], h.nbytes, 2) == 0  # device to host
+        assert hip.hipMemcpy(y.ctypes.data, bufs[2], y.nbytes, 2) == 0
+    finally:
+        for p in bufs:
+            hip.hipFree(p)
+    np.testing.assert_array_equal(h, pre)
+    np.testing.assert_array_equal(y, post)

@@ -103,18 +103,19 @@ welvet_status make(Swiglu *L, int bs, int in, int inter, int dtype, const float 
   return L->grow_ws(need);
 }
 
-// swiglu::forward swiglu.cpp:93-141 on L->x
-welvet_status forward(Swiglu *L) {
-  const hipStream_t s = L->stream;
-  WH_HIP(launch_forward(L->gate.dev(), L->bs, L->x, nullptr, 0, kLinear, L->g_pre, L->g_post, L->ws,
+// swiglu::forward swiglu.cpp:93-141: x [bs][in] -> h [bs][inter] (the
+// layer's pre), post [bs][in], enqueued on s
+welvet_status forward(Swiglu *L, const float *x, float *h, float *post, hipStream_t s) {
+  WH_HIP(launch_forward(L->gate.dev(), L->bs, x, nullptr, 0, kLinear, L->g_pre, L->g_post, L->ws,
                         L->ws_bytes, s));
-  WH_HIP(launch_forward(L->up.dev(), L->bs, L->x, nullptr, 0, kLinear, L->u_pre, L->u_post, L->ws,
+  WH_HIP(launch_forward(L->up.dev(), L->bs, x, nullptr, 0, kLinear, L->u_pre, L->u_post, L->ws,
                         L->ws_bytes, s));
-  WH_HIP(launch_swiglu_fwd(L->g_pre, L->u_post, (int64_t)L->bs * L->inter, L->h, s));
-  WH_HIP(launch_forward(L->down.dev(), L->bs, L->h, nullptr, 0, kLinear, L->d_pre, L->d_post, L->ws,
+  WH_HIP(launch_swiglu_fwd(L->g_pre, L->u_post, (int64_t)L->bs * L->inter, h, s));
+  WH_HIP(launch_forward(L->down.dev(), L->bs, h, nullptr, 0, kLinear, L->d_pre, post, L->ws,
                         L->ws_bytes, s));
   return ok();
 }
+welvet_status forward(Swiglu *L) { return forward(L, L->x, L->h, L->d_post, L->stream); }
 
 bool bad_dims(int32_t batch, int32_t seq, int32_t in, int32_t inter) {
   return batch <= 0 || seq <= 0 || in <= 0 || inter <= 0 || (int64_t)batch * seq > INT32_MAX;
@@ -216,5 +217,37 @@ welvet_status welvet_swiglu_normalbp_f32(int32_t batch, int32_t seq, int32_t inp
   *loss = h_loss;
   return ok();
 }
+
+// ---- resident SwiGLU (extension): the three stores stay mounted ----------
+
+welvet_status welvet_hip_swiglu_mount(int32_t rows, int32_t input_dim, int32_t intermediate_dim,
+                                      int32_t dtype, const float *Gate, const float *Up,
+                                      const float *Down, welvet_hip_swiglu **out) {
+  if (!out) return make_status(kInvalid, "swiglu: invalid argument");
+  *out = nullptr;
+  if (bad_dims(rows, 1, input_dim, intermediate_dim) || !Gate || !Up || !Down)
+    return make_status(kInvalid, "swiglu: invalid argument");
+  auto *L = new Swiglu();
+  welvet_status st = make(L, rows, input_dim, intermediate_dim, dtype, Gate, Up, Down);
+  if (st.code == 0 && hipStreamSynchronize(L->stream) != hipSuccess)
+    st = make_status(kInternal, "swiglu: mount failed");
+  if (st.code) {
+    delete L;
+    return st;
+  }
+  *out = reinterpret_cast<welvet_hip_swiglu *>(L);
+  return ok();
+}
+
+welvet_status welvet_hip_swiglu_forward_device(welvet_hip_swiglu *s, const float *d_x, float *d_pre,
+                                               float *d_post, void *stream) {
+  if (!s || !d_x || !d_pre || !d_post) return make_status(kInvalid, "swiglu: invalid argument");
+  if (((uintptr_t)d_x | (uintptr_t)d_pre | (uintptr_t)d_post) & 15)
+    return make_status(kInvalid, "device pointers must be 16-byte aligned");
+  auto *L = reinterpret_cast<Swiglu *>(s);
+  return forward(L, d_x, d_pre, d_post, (hipStream_t)stream);
+}
+
+void welvet_hip_swiglu_release(welvet_hip_swiglu *s) { delete reinterpret_cast<Swiglu *>(s); }
 
 }  // extern "C"

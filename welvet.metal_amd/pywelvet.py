@@ -116,6 +116,12 @@ def lib() -> C.CDLL:
         L.welvet_model_release.restype = None
         L.welvet_metal_blob_free.argtypes = [_bp]
         L.welvet_metal_blob_free.restype = None
+        L.welvet_hip_swiglu_mount.argtypes = [_i32] * 4 + [_f] * 3 + [C.POINTER(_vp)]
+        L.welvet_hip_swiglu_mount.restype = Status
+        L.welvet_hip_swiglu_forward_device.argtypes = [_vp] * 5
+        L.welvet_hip_swiglu_forward_device.restype = Status
+        L.welvet_hip_swiglu_release.argtypes = [_vp]
+        L.welvet_hip_swiglu_release.restype = None
         L.welvet_hip_volume_train_step_grad.argtypes = [_vp, _f, _i32, _f, _i32, C.c_double, _d,
                                                         _f, _f]
         L.welvet_hip_volume_train_step_grad.restype = Status
@@ -325,6 +331,33 @@ def chain_normalbp(kind, packed, x, grad_or_target, use_target, lr, child_act=-1
         return r
     check(st)
     return r
+
+
+class SwigluSession:
+    """welvet_hip_swiglu_mount / _forward_device / _release."""
+
+    def __init__(self, Gate, Up, Down, rows, dtype=1):
+        Gate, Up, Down = _f32(Gate), _f32(Up), _f32(Down)
+        self.inter, self.inn = Gate.shape
+        self.rows = rows
+        self.h = C.c_void_p()
+        check(lib().welvet_hip_swiglu_mount(rows, self.inn, self.inter, dtype, _fp(Gate), _fp(Up),
+                                            _fp(Down), C.byref(self.h)))
+
+    def forward_device(self, d_x, d_pre, d_post, stream=None):
+        """Device pointers (ints); enqueued on `stream` (a hipStream_t int)."""
+        return lib().welvet_hip_swiglu_forward_device(self.h, d_x, d_pre, d_post, stream)
+
+    def close(self):
+        if self.h:
+            lib().welvet_hip_swiglu_release(self.h)
+            self.h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 class Model:
