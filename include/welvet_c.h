@@ -296,7 +296,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *   13 dW kernel, every one bit-identical to the sequential FMA (the fp32
  *      MFMA accumulates each product with fmaf rounding, in k order): 2 MFMA
  *      with operands staged in LDS (out and in multiples of 128, else 1),
- *      1 MFMA with direct loads, 0 VALU [2] */
+ *      1 MFMA with direct loads, 0 VALU [2]
+ *   14 split-x GEMM for batch <= 16 on a 16-row tile (16x16x32 MFMA) instead
+ *      of the 32-row one [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

@@ -75,7 +75,8 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(gemv_waves=2, gemv_rows=16, cr=3), dict(gemv_waves=1, gemv_rows=1, pair_lut=0),
          dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4), dict(bf3_depth=2),
          dict(bf3_depth=3), dict(bf3_depth=3, gemm_occ=1), dict(bf3_cols=1),
-         dict(bf3_cols=1, gemm_occ=1), dict(dw_mfma=0)]
+         dict(bf3_cols=1, gemm_occ=1), dict(dw_mfma=0), dict(bf3_small=0),
+         dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -103,6 +104,36 @@ def test_forward_kernel_variants(oracle, knobs):
     finally:
         for k, v in old.items():
             pywelvet.set_tuning(k, v)
+
+
+@pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26])
+@pytest.mark.parametrize("batch", [5, 8, 13, 16, 17])
+def test_split_x_small_batch_tile(oracle, dtype, batch):
+    """The split-x GEMM's 16-row tile (16x16x32 MFMA, batch <= 16) and the
+    32-row tile it replaces: ragged N (304 rows), K not a multiple of the 64-deep stage,
+    both block widths and prefetch depths, forward and the dX that runs
+    through the store's transposed codes."""
+    rng = np.random.default_rng(1300 + 17 * dtype + batch)
+    W = rng.normal(0, 0.1, (304, 1040)).astype(np.float32)
+    if dtype == 16:
+        W = rng.uniform(-6, 6, (304, 1040)).astype(np.float32)
+    x = rng.normal(0, 1, (batch, 1040)).astype(np.float32)
+    gy = rng.normal(0, 1, (batch, 304)).astype(np.float32)
+    pre = rng.normal(0, 1, (batch, 304)).astype(np.float32)
+    Wd = oracle_weights(oracle, dtype, W)
+    _, rdX, rdW = oracle.backward(Wd, x, pre, gy, -1)
+    for knobs in (dict(bf3_small=1), dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2),
+                  dict(bf3_small=0)):
+        old = {k: pywelvet.set_tuning(k, v) for k, v in knobs.items()}
+        try:
+            check_forward(oracle, dtype, W, x)
+            with pywelvet.Session(W, batch=batch, act=-1, dtype=dtype) as s:
+                dX, dW = s.backward(x, pre, gy)
+            assert_close(dX, rdX, 304, f"dX {knobs}")
+            assert_bit_equal(dW, rdW, f"dW {knobs}")
+        finally:
+            for k, v in old.items():
+                pywelvet.set_tuning(k, v)
 
 
 def test_every_gemv_shape_knob_launches(oracle):

@@ -1346,6 +1346,167 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
   }
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// The split-x GEMM for batch <= 16: one 16-row tile on
+// v_mfma_f32_16x16x32_bf16, where the 32-row MFMA would spend three quarters
+// of its work on padding rows at batch 8.  Same units, stream-K shares, x
+// split and weight decode as gemm_bf3_kernel; per stage a lane (j = lane % 16,
+// g = lane / 16) holds for each 16-column group the 16 consecutive weights
+// k = 16 g .. 16 g + 15 of column j, and MFMA step q in {0, 1} takes
+// k = 16 g + 8 q + i (i < 8) from both operands: a permutation of the stage's
+// k order, the same on both sides.  D lane (j, g) holds column j, rows
+// 4 g .. 4 g + 3.
+template <int BK, int D, int NC>
+__global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
+  using K3 = B3<BK>;
+  constexpr int BM = 16, BN = 128 * NC, NW = K3::kWords / 2, NP = K3::kParts;
+  constexpr int CG = 2 * NC;          // 16-column groups per wave
+  constexpr int XE = BM * kBK / 256;  // 4 x values per thread per stage
+  constexpr int XT = kBK / XE;        // 16 threads per x row
+  static_assert(XE == 4 && (NW == 2 || NW == 4), "16-row split-x layout");
+  __shared__ uint16_t Xs[2][3][BM][kBf3Row];
+  __shared__ uint2 t3[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  if constexpr (BK == BK_NF4) {
+    if (tid < 16) {
+      const float t = kNf4Tab[tid];
+      const uint32_t hi = f2u(t) & 0xffff0000u;
+      const float r = t - u2f(hi);
+      const uint32_t mid = f2u(r) & 0xffff0000u;
+      const uint32_t lo = f2u(r - u2f(mid));
+      t3[tid] = make_uint2((hi >> 16) | mid, lo >> 16);
+    }
+  }
+  const int T = a.gx * a.gy * a.nst;
+  int it = blockIdx.x * a.per_block;
+  const int it_end = min(T, it + a.per_block);
+  const int first_tile = it / a.nst;
+  const int xm = tid / XT, xk = (tid % XT) * XE;  // xm < 16, xk < 64
+  uint32_t wr[D][CG][NW];
+  float xf[D][XE];
+  uint32_t xin[D];
+  auto unit_m0 = [&](int u) { return (u / a.nst / a.gx) * BM; };
+  auto unit_n0 = [&](int u) { return (u / a.nst % a.gx) * BN; };
+  auto load_w = [&](int u, uint32_t (&w)[CG][NW]) {
+    const int n0 = unit_n0(u), k0 = (u % a.nst) * kBK;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const int row = min(n0 + wave * 32 * NC + c * 16 + j, a.N - 1);
+      const uint8_t *src = a.body + (int64_t)row * a.row_bytes + (k0 + 16 * g) * K3::kBits / 8;
+      if constexpr (NW == 4) {
+        const uint4 v = *(const uint4 *)src;
+        w[c][0] = v.x; w[c][1] = v.y; w[c][2] = v.z; w[c][3] = v.w;
+      } else {
+        const uint2 v = *(const uint2 *)src;
+        w[c][0] = v.x; w[c][1] = v.y;
+      }
+    }
+  };
+  auto load_x = [&](int u, float (&xv)[XE], uint32_t &in_mask) {
+    const int m0 = unit_m0(u), k0 = (u % a.nst) * kBK;
+    const bool in = m0 + xm < a.M && k0 + xk < a.K;
+    in_mask = in ? ~0u : 0u;
+    const float4 v = *(const float4 *)(a.A + (int64_t)(in ? m0 + xm : 0) * a.K + (in ? k0 + xk : 0));
+    xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+  };
+  auto store_x = [&](int buf, const float (&xv)[XE], uint32_t in_mask) {
+    uint32_t wp[3][2];
+#pragma unroll
+    for (int i = 0; i < XE; i += 2) {
+      uint32_t part[3][2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = u2f(f2u(xv[i + e]) & in_mask);
+        const uint32_t hi = f2u(v) & 0xffff0000u;
+        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const uint32_t mid = f2u(r) & 0xffff0000u;
+        part[0][e] = hi;
+        part[1][e] = mid;
+        part[2][e] = f2u(r - u2f(mid));
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) wp[p][i / 2] = __builtin_amdgcn_perm(part[p][1], part[p][0], 0x07060302u);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) *(uint2 *)&Xs[buf][p][xm][xk] = make_uint2(wp[p][0], wp[p][1]);
+  };
+  auto mfma_step = [&](floatx4 (&acc)[CG], int buf, int q, const bf16x8 (&bv)[CG][NP]) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[buf][p][j][16 * g + 8 * q]);
+#pragma unroll
+      for (int c = 0; c < CG; ++c)
+#pragma unroll
+        for (int wp = 0; wp < NP; ++wp)
+          if (p + wp <= 2) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[c][wp], acc[c], 0, 0, 0);
+    }
+  };
+  floatx4 acc[CG];
+  int buf = 0;
+  const int last = max(it, it_end - 1);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load_w(min(it + d, last), wr[d]);
+    load_x(min(it + d, last), xf[d], xin[d]);
+  }
+  store_x(0, xf[0], xin[0]);
+  __syncthreads();
+  for (int u0 = it; u0 < it_end; u0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int u = u0 + d;
+      if (u >= it_end) break;
+      const int t = u / a.nst, st = u - t * a.nst;
+      if (u == it || st == 0) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
+      }
+      if constexpr (NP == 1) {
+        bf16x8 bv[2][CG][1];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int c = 0; c < CG; ++c) {
+            bf16x8 pp[1];
+            bf3_weights<BK>(wr[d][c], q, t3, pp);
+            bv[q][c][0] = pp[0];
+          }
+        load_w(min(u + D, last), wr[d]);
+        load_x(min(u + D, last), xf[d], xin[d]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) mfma_step(acc, buf, q, bv[q]);
+      } else {
+        load_x(min(u + D, last), xf[d], xin[d]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          bf16x8 bv[CG][NP];
+#pragma unroll
+          for (int c = 0; c < CG; ++c) bf3_weights<BK>(wr[d][c], q, t3, bv[c]);
+          mfma_step(acc, buf, q, bv);
+        }
+        load_w(min(u + D, last), wr[d]);
+      }
+      store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
+      __syncthreads();
+      buf ^= 1;
+      if (st == a.nst - 1 || u + 1 == it_end) {
+        // rows 4 g .. 4 g + 3 of the tile; a group wholly past M is never read
+        float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * BN);
+        if (4 * g < a.M - unit_m0(u)) {
+#pragma unroll
+          for (int c = 0; c < CG; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[(4 * g + r) * BN + wave * 32 * NC + c * 16 + j] = acc[c][r];
+        }
+      }
+    }
+  }
+}
+
 // Sum of a tile's stream-K partials in workgroup order (f64).  Grid: x =
 // tile, y = 1024-element slice of the tile; each thread adds four adjacent
 // outputs with float4 loads.  The forward applies bias + activation, dX
@@ -1816,7 +1977,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 2};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 2, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -1927,7 +2088,8 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
   if (bk >= 0) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
     const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
-    SkPlan p = plan_sk(M, K, N, M <= 32 ? 32 : 64, bn, occ);
+    const int bm = (M <= 16 && g_tune[kTuneBf3Small] != 0) ? 16 : M <= 32 ? 32 : 64;
+    SkPlan p = plan_sk(M, K, N, bm, bn, occ);
     p.bf3 = true;
     return p;
   }
@@ -2010,7 +2172,11 @@ size_t forward_workspace_bytes(const DevStore &w, int batch) {
 hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
   const int dep = g_tune[kTuneBf3Depth];
 #define WH_GB(BK, D1)                                                                 \
-  if (p.bm == 32) {                                                                   \
+  if (p.bm == 16) {                                                                   \
+    if (p.bn == 128) gemm_bf3s_kernel<BK, D1, 1><<<p.blocks, 256, 0, s>>>(a);          \
+    else if (dep == 2 || D1 == 2) gemm_bf3s_kernel<BK, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    else gemm_bf3s_kernel<BK, 1, 2><<<p.blocks, 256, 0, s>>>(a);                       \
+  } else if (p.bm == 32) {                                                            \
     if (p.bn == 128) gemm_bf3_kernel<BK, 1, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
     else if (dep == 3) gemm_bf3_kernel<BK, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);       \
     else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a); \

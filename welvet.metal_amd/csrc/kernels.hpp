@@ -105,11 +105,13 @@ void set_forward_path(int path);
 // prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
 // width (0: 256 output columns, 1: 128).  13 dW kernel, all bit-identical to the
 // sequential FMA: 2 fp32 MFMA with operands staged in LDS (shapes of whole
-// 128-tiles; others take 1), 1 fp32 MFMA with direct loads, 0 VALU.
+// 128-tiles; others take 1), 1 fp32 MFMA with direct loads, 0 VALU.  14 the
+// split-x GEMM's 16-row tile on the 16x16x32 MFMA for batch <= 16 (1 on).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
-  kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kNumTune = 14
+  kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
+  kNumTune = 15
 };
 int set_tuning(int key, int value);
 
