@@ -2370,10 +2370,14 @@ size_t backward_workspace_bytes(const DevStore &w, int batch) {
 }
 
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
-                           const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
+                           const float *gy, int act, float *dpre_buf, float *dX, float *dW, int *flag,
                            void *ws, size_t ws_bytes, hipStream_t s) {
   const int64_t ny = (int64_t)batch * w.rows;
-  act_deriv_kernel<<<blocks_for(ny), 256, 0, s>>>(gy, pre, ny, act, dpre);
+  // dpre = gy * act'(pre); act' is 1 for Linear (and the ids act_prime
+  // treats as Linear), where gy * 1 = gy bit for bit: the kernel is skipped
+  const bool identity = act < kReLU || act > kReLU2;
+  const float *dpre = identity ? gy : dpre_buf;
+  if (!identity) act_deriv_kernel<<<blocks_for(ny), 256, 0, s>>>(gy, pre, ny, act, dpre_buf);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int route = dx_route(w, batch);
