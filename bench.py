@@ -394,7 +394,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed steps per case before the timed ones (the GPU clocks settle)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of cases: fp8b1,nf4b1,fp8b64,nf4b64")
     ap.add_argument("--no-configs", action="store_true",
