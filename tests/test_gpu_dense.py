@@ -106,6 +106,20 @@ def test_forward_kernel_variants(oracle, knobs):
             pywelvet.set_tuning(k, v)
 
 
+@pytest.mark.parametrize("dtype", [16, 26, 14, 15])
+@pytest.mark.parametrize("cols", [8448, 11008, 8232])
+def test_long_row_gemv(oracle, dtype, cols):
+    """Batch-1 GEMV on rows of three or more waves of two chunks per lane
+    (the 8-rows-per-block default for 4-bit formats): ragged row count, K
+    just past the switch-over and not a multiple of the chunk."""
+    rng = np.random.default_rng(1400 + dtype + cols)
+    W = rng.normal(0, 0.1, (203, cols)).astype(np.float32)
+    if dtype == 16:
+        W = rng.uniform(-6, 6, (203, cols)).astype(np.float32)
+    x = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    check_forward(oracle, dtype, W, x, act=1, bias=rng.normal(0, 0.1, 203))
+
+
 @pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26])
 @pytest.mark.parametrize("batch", [5, 8, 13, 16, 17])
 def test_split_x_small_batch_tile(oracle, dtype, batch):
