@@ -168,6 +168,19 @@ WELVET_API welvet_status welvet_hip_dense_mount_device(int32_t batch, int32_t in
                                                        size_t bias_len,
                                                        welvet_dense_session **sess);
 
+/* welvet_dense_mount from a store snapshot instead of f32 values: the native
+ * bytes in the reference's WeightStore::native layout (4-byte f32 min header
+ * for the unsigned types; the f32 bytes for Float32) and the store's scale,
+ * taken byte for byte as the model-session import does
+ * (reference src/interop/model_session.cpp:128-151 read_store).  Code 1 when
+ * native_len is not the layout's size for [out*in] or the scale is not finite. */
+WELVET_API welvet_status welvet_hip_dense_mount_native(int32_t batch, int32_t in, int32_t out,
+                                                       int32_t act, int32_t dtype,
+                                                       const uint8_t *native, size_t native_len,
+                                                       float scale, const double *bias,
+                                                       size_t bias_len,
+                                                       welvet_dense_session **sess);
+
 /* Forward on device pointers (16-byte aligned) enqueued on `stream`
  * (a hipStream_t; NULL = the HIP null stream); returns once enqueued. */
 WELVET_API welvet_status welvet_hip_dense_forward_device(welvet_dense_session *s, const float *d_x,

@@ -863,8 +863,11 @@ float or_act_prime(float v, int act) {
  * Go contract pre = fl32(sum_k f64(W)*f64(x)) in k order, then
  * welvet_dense_bias_act :87-105: pre = fl32(f64(pre) + bias) for o < bias_len,
  * post = act(pre).  Wd is the decode_row_f64 matrix [out][in]. */
+/* Outputs are independent and each keeps its k order, so splitting the
+ * (b, o) pairs over OpenMP threads changes no bit of the result. */
 void or_dense_forward(int batch, int in, int out, int act, const double *Wd, const double *bias,
                       int64_t bias_len, const float *x, float *pre, float *post) {
+#pragma omp parallel for collapse(2) schedule(static)
   for (int b = 0; b < batch; ++b) {
     for (int o = 0; o < out; ++o) {
       double acc = 0;
@@ -882,24 +885,37 @@ void or_dense_forward(int batch, int in, int out, int act, const double *Wd, con
 /* welvet_dense_act_deriv :107-119, welvet_dense_matvect_softdouble_batch
  * :121-153 (dX = fl32(sum_o W[o,i]*dpre[b,o]) in o order) and
  * welvet_dense_outer_batch :155-178 (dW[o,i] = sequential fp32 FMA over b). */
+/* Each dX[b][i] is summed over o in ascending order and each dW[o][i] over b
+ * in ascending order; the loops below keep those orders (the running sums of
+ * a whole row advance together, one o or one b at a time), so the threads
+ * and the row-wise traversal change no bit of the result. */
 void or_dense_backward(int batch, int in, int out, int act, const double *Wd, const float *x,
                        const float *pre, const float *gy, float *dpre, float *dX, float *dW) {
   const int64_t ny = (int64_t)batch * out;
   for (int64_t j = 0; j < ny; ++j) dpre[j] = gy[j] * or_act_prime(pre[j], act);
-  for (int b = 0; b < batch; ++b) {
-    for (int i = 0; i < in; ++i) {
-      double acc = 0;
-      for (int o = 0; o < out; ++o)
-        acc += Wd[(int64_t)o * in + i] * (double)dpre[(int64_t)b * out + o];
-      dX[(int64_t)b * in + i] = (float)acc;
+#pragma omp parallel
+  {
+    double *acc = (double *)malloc(sizeof(double) * (size_t)in);
+#pragma omp for schedule(static)
+    for (int b = 0; b < batch; ++b) {
+      for (int i = 0; i < in; ++i) acc[i] = 0;
+      for (int o = 0; o < out; ++o) {
+        const double g = (double)dpre[(int64_t)b * out + o];
+        const double *row = Wd + (int64_t)o * in;
+        for (int i = 0; i < in; ++i) acc[i] += row[i] * g;
+      }
+      for (int i = 0; i < in; ++i) dX[(int64_t)b * in + i] = (float)acc[i];
     }
+    free(acc);
   }
+#pragma omp parallel for schedule(static)
   for (int o = 0; o < out; ++o) {
-    for (int i = 0; i < in; ++i) {
-      float acc = 0.0f;
-      for (int b = 0; b < batch; ++b)
-        acc = fmaf(dpre[(int64_t)b * out + o], x[(int64_t)b * in + i], acc);
-      dW[(int64_t)o * in + i] = acc;
+    float *row = dW + (int64_t)o * in;
+    for (int i = 0; i < in; ++i) row[i] = 0.0f;
+    for (int b = 0; b < batch; ++b) {
+      const float g = dpre[(int64_t)b * out + o];
+      const float *xb = x + (int64_t)b * in;
+      for (int i = 0; i < in; ++i) row[i] = fmaf(g, xb[i], row[i]);
     }
   }
 }
@@ -1024,6 +1040,20 @@ void or_dense_forward_native(int batch, int in, int out, int act, int dtype, con
     free(row);
   }
   (void)threads;
+}
+
+/* Bulk scalar-codec decode: kind 0 f16, 1 bf16, 2 e4m3, 3 e5m2, 4 fp4, into
+ * an f32 array (memory keeps signaling-NaN payloads bit for bit). */
+void or_decode_many(int kind, const uint32_t *codes, int64_t n, float *out) {
+  for (int64_t i = 0; i < n; ++i) {
+    switch (kind) {
+    case 0: out[i] = or_f16_to_f32((uint16_t)codes[i]); break;
+    case 1: out[i] = or_bf16_to_f32((uint16_t)codes[i]); break;
+    case 2: out[i] = or_e4m3_to_f32((uint8_t)codes[i]); break;
+    case 3: out[i] = or_e5m2_to_f32((uint8_t)codes[i]); break;
+    default: out[i] = or_fp4_to_f32((uint8_t)codes[i]); break;
+    }
+  }
 }
 
 /* Bulk scalar-codec sweep for exhaustive checks: kind 0 f16, 1 bf16, 2 e4m3,

@@ -88,6 +88,8 @@ class Oracle:
         L.or_dense_forward_native.restype = None
         L.or_encode_many.argtypes = [_i, _vp, _i64, _vp]
         L.or_encode_many.restype = None
+        L.or_decode_many.argtypes = [_i, _vp, _i64, _vp]
+        L.or_decode_many.restype = None
         L.or_swiglu_h.argtypes = [_vp, _vp, _i64, _vp]
         L.or_swiglu_h.restype = None
         L.or_swiglu_split.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
@@ -138,6 +140,14 @@ class Oracle:
         x = np.ascontiguousarray(x, np.float32)
         out = np.zeros(x.size, np.uint16 if kind in (0, 1) else np.uint8)
         self.lib.or_encode_many(kind, _ptr(x), x.size, _ptr(out))
+        return out
+
+    def decode_many(self, kind: int, codes) -> np.ndarray:
+        """Scalar-codec decode of every code (kind 0 f16, 1 bf16, 2 e4m3,
+        3 e5m2, 4 fp4), written to memory: signaling-NaN payloads survive."""
+        c = np.ascontiguousarray(codes, np.uint32)
+        out = np.zeros(c.size, np.float32)
+        self.lib.or_decode_many(kind, _ptr(c), c.size, _ptr(out))
         return out
 
     # -- dense ----------------------------------------------------------------
@@ -347,6 +357,8 @@ class Reference:
         L.ref_decode_f64.restype = _i
         L.ref_encode_many.argtypes = [_i, _vp, C.c_long, _vp]
         L.ref_encode_many.restype = None
+        L.ref_decode_many.argtypes = [_i, _vp, C.c_long, _vp]
+        L.ref_decode_many.restype = None
         for nm, ct in (("f16", C.c_uint16), ("bf16", C.c_uint16), ("e4m3", C.c_uint8),
                        ("e5m2", C.c_uint8), ("fp4", C.c_uint8)):
             dec = getattr(L, f"ref_{nm}_to_f32")
@@ -383,6 +395,12 @@ class Reference:
         x = np.ascontiguousarray(x, np.float32)
         out = np.zeros(x.size, np.uint16 if kind in (0, 1) else np.uint8)
         self.lib.ref_encode_many(kind, _ptr(x), x.size, _ptr(out))
+        return out
+
+    def decode_many(self, kind: int, codes) -> np.ndarray:
+        c = np.ascontiguousarray(codes, np.uint32)
+        out = np.zeros(c.size, np.float32)
+        self.lib.ref_decode_many(kind, _ptr(c), c.size, _ptr(out))
         return out
 
 

@@ -72,6 +72,22 @@ REF_API float ref_e5m2_to_f32(unsigned char b) { return welvet::fp8e5m2_to_float
 REF_API unsigned char ref_f32_to_fp4(float f) { return welvet::float32_to_fp4(f); }
 REF_API float ref_fp4_to_f32(unsigned char c) { return welvet::fp4_to_float32(c); }
 
+// Decodes n codes into an f32 array (kind as below).  Writing the result to
+// memory keeps every bit, including signaling-NaN payloads, which a scalar
+// float return converted to a double by a caller would quiet.
+REF_API void ref_decode_many(int kind, const unsigned int *codes, long n, float *out) {
+  for (long i = 0; i < n; ++i) {
+    const unsigned int c = codes[i];
+    switch (kind) {
+    case 0: out[i] = welvet::float16_to_float32(static_cast<unsigned short>(c)); break;
+    case 1: out[i] = welvet::bfloat16_to_float32(static_cast<unsigned short>(c)); break;
+    case 2: out[i] = welvet::fp8e4m3_to_float32(static_cast<unsigned char>(c)); break;
+    case 3: out[i] = welvet::fp8e5m2_to_float32(static_cast<unsigned char>(c)); break;
+    default: out[i] = welvet::fp4_to_float32(static_cast<unsigned char>(c)); break;
+    }
+  }
+}
+
 // Bulk scalar-codec sweep for exhaustive checks: kind 0 f16, 1 bf16, 2 e4m3,
 // 3 e5m2, 4 fp4; encodes n floats into out (uint16 for kinds 0-1, else uint8).
 REF_API void ref_encode_many(int kind, const float *in, long n, void *out) {

@@ -192,12 +192,18 @@ def test_activations_with_bias(oracle, act):
         check_forward(oracle, 26, W, xb, act=act, bias=bias)
 
 
-@pytest.mark.parametrize("dtype,batch", [(4, 1), (26, 1), (4, 64), (26, 64), (16, 8), (5, 32)])
+@pytest.mark.parametrize("dtype,batch", [(4, 1), (26, 1), (4, 64), (26, 64), (16, 1), (16, 8),
+                                         (16, 64), (5, 32)])
 def test_forward_headline_shapes(oracle, dtype, batch):
-    """4096 -> 11008 and 11008 -> 4096 (the LLM-MLP pair) with N(0, 0.02) weights."""
+    """4096 -> 11008 and 11008 -> 4096 (the LLM-MLP pair) with N(0, 0.02)
+    weights; FP4 (no scale: N(0, 0.02) would encode every weight to code 0)
+    with U(-6, 6), which spans its whole grid."""
     rng = np.random.default_rng(0x5EED0003 + batch)
     for out, inn in ((11008, 4096), (4096, 11008)):
-        W = rng.normal(0, 0.02, (out, inn)).astype(np.float32)
+        if dtype == 16:
+            W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+        else:
+            W = rng.normal(0, 0.02, (out, inn)).astype(np.float32)
         x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
         check_forward(oracle, dtype, W, x)
 

@@ -254,6 +254,79 @@ def test_set_signed_integer_quantizer(oracle):
             assert oracle.decode(dtype, r, scale, n)[3] == np.float32(want), (dtype, v)
 
 
+# (dtype, largest code, signed): the fixed-scale re-encode of
+# ops_storage.metal:636-654 (n-bit), :692-762 (integers), :748-755 (quant_u64)
+UNSIGNED_SET = [(13, 255), (12, 65535), (15, 15), (18, 3), (29, 63), (31, 31), (33, 7)]
+SIGNED_SET = [(28, 31), (27, 31), (30, 15), (32, 3), (17, 1)]
+
+
+def _q_of(oracle, dtype, raw, s, mn, n, i):
+    """The integer code of element i from its decode q*s + min (s a power of two)."""
+    return (float(oracle.decode(dtype, raw, s, n)[i]) - mn) / s
+
+
+@pytest.mark.parametrize("dtype,qmax", UNSIGNED_SET, ids=[DTYPE_NAMES[d] for d, _ in UNSIGNED_SET])
+def test_set_unsigned_closed_form(oracle, dtype, qmax):
+    """Unsigned re-encode with the stored min m and a power-of-two scale s:
+    code = clamp(round-half-away((v - m) / s), 0, qmax).  Values exactly half
+    way between two codes (even and odd lower code alike) go up, values just
+    below half way go down, and both clamp bounds hold; ties-to-even, a
+    truncation, a dropped min or an off-by-one bound fails."""
+    n, i = 16, 5
+    s, mn = 2.0 ** -4, -1.25
+    raw = np.zeros(oracle.native_bytes(dtype, n), np.uint8)
+    raw[:4] = np.frombuffer(np.float32(mn).tobytes(), np.uint8)
+    cases = [(q + 0.5, q + 1) for q in range(0, min(qmax, 6))]
+    cases += [(q + 0.5 - 2.0 ** -8, q) for q in range(0, min(qmax, 6))]
+    cases += [(qmax + 0.5, qmax), (qmax + 40.0, qmax), (-0.5 + 2.0 ** -8, 0), (-0.5, 0), (-30.0, 0), (0.0, 0)]
+    for t, want in cases:
+        r = raw.copy()
+        v = np.float32(mn + t * s)
+        assert float(v) == mn + t * s  # the input is exact, so only the rounding rule decides
+        assert oracle.set(dtype, r, s, i, n, float(v)) == 0
+        assert _q_of(oracle, dtype, r, s, mn, n, i) == want, (DTYPE_NAMES[dtype], t, want)
+        assert np.count_nonzero(r[:4] != raw[:4]) == 0  # the min header is kept
+
+
+@pytest.mark.parametrize("dtype,qmax", SIGNED_SET, ids=[DTYPE_NAMES[d] for d, _ in SIGNED_SET])
+def test_set_signed_nbit_closed_form(oracle, dtype, qmax):
+    """Signed n-bit re-encode (Int6 / FP6 / Int5 / Int3, two's complement; Int2
+    stored as q + 2): code = clamp(round-half-away(v / s), -qmax - 1, qmax)."""
+    n, i = 16, 9
+    s = 2.0 ** -3
+    raw = np.zeros(oracle.native_bytes(dtype, n), np.uint8)
+    cases = []
+    for q in range(0, min(qmax, 5)):
+        cases += [(q + 0.5, q + 1), (-(q + 0.5), -(q + 1)), (q + 0.5 - 2.0 ** -8, q),
+                  (-(q + 0.5 - 2.0 ** -8), -q)]
+    cases += [(qmax + 0.5, qmax), (qmax + 100.0, qmax), (-(qmax + 1.5), -qmax - 1),
+              (-(qmax + 100.0), -qmax - 1)]
+    for t, want in cases:
+        r = raw.copy()
+        assert oracle.set(dtype, r, s, i, n, t * s) == 0
+        got = float(oracle.decode(dtype, r, s, n)[i]) / s
+        assert got == want, (DTYPE_NAMES[dtype], t, got, want)
+        others = np.arange(n) != i
+        assert np.all(oracle.decode(dtype, r, s, n)[others] == oracle.decode(dtype, raw, s, n)[others])
+
+
+def test_set_ternary_and_binary_thresholds(oracle):
+    """Ternary: v/s > 0.5 -> +s, < -0.5 -> -s, else 0 (0.5 itself is 0);
+    Binary: v >= 0 -> +s, else -s (ops_storage.metal set_weight_at)."""
+    n, s = 8, 0.25
+    raw = np.zeros(oracle.native_bytes(19, n), np.uint8)
+    for t, want in ((0.5, 0.0), (0.5 + 2.0 ** -10, s), (-0.5, 0.0), (-0.5 - 2.0 ** -10, -s),
+                    (3.0, s), (-3.0, -s), (0.0, 0.0)):
+        r = raw.copy()
+        oracle.set(19, r, s, 2, n, t * s)
+        assert oracle.decode(19, r, s, n)[2] == np.float32(want), t
+    raw = np.zeros(oracle.native_bytes(20, n), np.uint8)
+    for v, want in ((0.0, s), (-0.0, s), (1e-30, s), (-1e-30, -s), (-5.0, -s)):
+        r = raw.copy()
+        oracle.set(20, r, s, 3, n, v)
+        assert oracle.decode(20, r, s, n)[3] == np.float32(want), v
+
+
 def test_set_saturating_clamp_bounds(oracle):
     """The float clamp bounds 2147483647.0f and 4294967295.0f are 2^31 and 2^32:
     the following conversion saturates (arm64)."""

@@ -369,11 +369,23 @@ welvet_status forward_device(welvet_dense_session *s, const float *x, float *pre
   return ok();
 }
 
+// Where a mount's weights come from: f32 values on the host or the device
+// (encoded on the device), or a store snapshot in the reference's native
+// byte layout (taken byte for byte).
+struct WeightSource {
+  enum Kind { kHostF32, kDeviceF32, kNative } kind = kHostF32;
+  const float *f32 = nullptr;
+  const uint8_t *raw = nullptr;
+  size_t raw_len = 0;
+  float scale = 1.0f;
+};
+
 // session_mount session.cpp:37-84 (dtype -> 2, dims/batch -> 1)
 welvet_status mount(int32_t batch, int32_t in, int32_t out, int32_t act, int32_t dtype,
-                    const float *W_init, const double *bias, size_t bias_len,
-                    welvet_dense_session **sess, bool device_init_ptr = false) {
-  if (!sess || !W_init) return make_status(kInvalid, "invalid argument");
+                    const WeightSource &src, const double *bias, size_t bias_len,
+                    welvet_dense_session **sess) {
+  if (!sess || (src.kind == WeightSource::kNative ? !src.raw : !src.f32))
+    return make_status(kInvalid, "invalid argument");
   if (dtype < 0 || dtype >= kNumDTypes)
     return make_status(kUnsupported, "dense HIP unsupported dtype %d", dtype);
   welvet_status st = require_device();
@@ -387,8 +399,17 @@ welvet_status mount(int32_t batch, int32_t in, int32_t out, int32_t act, int32_t
     delete s;
     return make_status(kInternal, "hipStreamCreate failed");
   }
-  st = device_init_ptr ? store_make(&s->W, dtype, out, in, W_init, s->stream)
-                       : store_from_host(&s->W, dtype, out, in, W_init, s->stream);
+  if (src.kind == WeightSource::kDeviceF32) {
+    st = store_make(&s->W, dtype, out, in, src.f32, s->stream);
+  } else if (src.kind == WeightSource::kHostF32) {
+    st = store_from_host(&s->W, dtype, out, in, src.f32, s->stream);
+  } else if (dtype == kFloat32) {
+    st = src.raw_len % 4 ? make_status(kInvalid, "native store payload length mismatch")
+                         : store_from_native(&s->W, dtype, out, in, 1.0f, (const float *)src.raw,
+                                             src.raw_len / 4, nullptr, 0, s->stream);
+  } else {
+    st = store_from_native(&s->W, dtype, out, in, src.scale, nullptr, 0, src.raw, src.raw_len, s->stream);
+  }
   if (!st.code) st = store_set_bias(&s->W, bias, bias_len, s->stream);
   if (!st.code) st = session_alloc_io(s);
   if (!st.code && hipStreamSynchronize(s->stream) != hipSuccess)
@@ -460,7 +481,9 @@ welvet_status welvet_metal_init(void) {
   // probe: encode and decode two values through the device codec
   const float w[2] = {0.5f, -0.25f};
   welvet_dense_session *s = nullptr;
-  st = mount(1, 2, 1, kLinear, kFP8E4M3, w, nullptr, 0, &s);
+  WeightSource src;
+  src.f32 = w;
+  st = mount(1, 2, 1, kLinear, kFP8E4M3, src, nullptr, 0, &s);
   if (st.code) return st;
   float back[2] = {0, 0};
   st = welvet_hip_dense_export_f32(s, back);
@@ -478,7 +501,9 @@ int32_t welvet_metal_available(void) {
 welvet_status welvet_dense_mount(int32_t batch, int32_t in, int32_t out, int32_t act, int32_t dtype,
                                  const float *W_init, const double *bias, size_t bias_len,
                                  welvet_dense_session **sess) {
-  return mount(batch, in, out, act, dtype, W_init, bias, bias_len, sess);
+  WeightSource src;
+  src.f32 = W_init;
+  return mount(batch, in, out, act, dtype, src, bias, bias_len, sess);
 }
 
 welvet_status welvet_hip_dense_mount_device(int32_t batch, int32_t in, int32_t out, int32_t act,
@@ -486,7 +511,22 @@ welvet_status welvet_hip_dense_mount_device(int32_t batch, int32_t in, int32_t o
                                             const double *bias, size_t bias_len,
                                             welvet_dense_session **sess) {
   if ((uintptr_t)d_W_init & 15) return make_status(kInvalid, "device pointers must be 16-byte aligned");
-  return mount(batch, in, out, act, dtype, d_W_init, bias, bias_len, sess, true);
+  WeightSource src;
+  src.kind = WeightSource::kDeviceF32;
+  src.f32 = d_W_init;
+  return mount(batch, in, out, act, dtype, src, bias, bias_len, sess);
+}
+
+welvet_status welvet_hip_dense_mount_native(int32_t batch, int32_t in, int32_t out, int32_t act,
+                                            int32_t dtype, const uint8_t *native, size_t native_len,
+                                            float scale, const double *bias, size_t bias_len,
+                                            welvet_dense_session **sess) {
+  WeightSource src;
+  src.kind = WeightSource::kNative;
+  src.raw = native;
+  src.raw_len = native_len;
+  src.scale = scale;
+  return mount(batch, in, out, act, dtype, src, bias, bias_len, sess);
 }
 
 welvet_status welvet_dense_execute(welvet_dense_session *s, const float *x, float *pre, float *post) {
@@ -500,7 +540,9 @@ welvet_status welvet_dense_forward_f32(int32_t batch, int32_t in, int32_t out, i
                                        const double *bias, size_t bias_len, const float *x,
                                        float *pre, float *post) {
   welvet_dense_session *s = nullptr;
-  welvet_status st = mount(batch, in, out, act, dtype, W_init, bias, bias_len, &s);
+  WeightSource src;
+  src.f32 = W_init;
+  welvet_status st = mount(batch, in, out, act, dtype, src, bias, bias_len, &s);
   if (st.code) return st;
   st = execute(s, x, pre, post);
   session_free(s);
@@ -518,7 +560,9 @@ welvet_status welvet_dense_normalbp_f32(int32_t batch, int32_t in, int32_t out, 
     return make_status(kInvalid, "invalid argument");
   if (dtype < 0 || dtype >= kNumDTypes) return make_status(kInvalid, "bad dtype %d", dtype);
   welvet_dense_session *s = nullptr;
-  welvet_status st = mount(batch, in, out, act, dtype, W_init, bias, bias_len, &s);
+  WeightSource src;
+  src.f32 = W_init;
+  welvet_status st = mount(batch, in, out, act, dtype, src, bias, bias_len, &s);
   if (st.code) return st;
   const int64_t ny = (int64_t)batch * out, nx = (int64_t)batch * in, nw = (int64_t)out * in;
   hipStream_t strm = s->stream;

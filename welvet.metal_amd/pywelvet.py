@@ -134,6 +134,9 @@ def lib() -> C.CDLL:
         L.welvet_hip_dense_mount_device.argtypes = [_i32] * 5 + [_vp, _d, C.c_size_t,
                                                              C.POINTER(_vp)]
         L.welvet_hip_dense_mount_device.restype = Status
+        L.welvet_hip_dense_mount_native.argtypes = [_i32] * 5 + [_u8, C.c_size_t, C.c_float, _d,
+                                                             C.c_size_t, C.POINTER(_vp)]
+        L.welvet_hip_dense_mount_native.restype = Status
         L.welvet_hip_dense_forward_device.argtypes = [_vp, _vp, _vp, _vp, _vp]
         L.welvet_hip_dense_forward_device.restype = Status
         L.welvet_hip_dense_native.argtypes = [_vp, _u8, C.c_size_t, C.POINTER(C.c_size_t), _f]
@@ -417,19 +420,32 @@ class Model:
 class Session:
     """welvet_dense_mount / execute / release plus the welvet_hip_ extensions."""
 
-    def __init__(self, W, batch, act=-1, dtype=1, bias=None):
-        W = _f32(W)
-        self.out, self.inn = W.shape
+    def __init__(self, W, batch, act=-1, dtype=1, bias=None, native=None):
+        """W: f32 [out][in] encoded into dtype, or, with native=(bytes, scale),
+        the shape (out, in) of a store taken byte for byte from a snapshot in
+        the reference layout (welvet_hip_dense_mount_native)."""
+        self.h = None
+        if native is None:
+            W = _f32(W)
+            self.out, self.inn = W.shape
+        else:
+            self.out, self.inn = W
         self.batch = batch
         self.dtype = dtype
         b = None if bias is None else np.ascontiguousarray(bias, np.float64)
         h = _vp()
-        check(lib().welvet_dense_mount(batch, self.inn, self.out, act, dtype, _fp(W), _dp(b),
-                                       0 if b is None else b.size, C.byref(h)))
+        if native is None:
+            check(lib().welvet_dense_mount(batch, self.inn, self.out, act, dtype, _fp(W), _dp(b),
+                                           0 if b is None else b.size, C.byref(h)))
+        else:
+            raw = np.ascontiguousarray(native[0], np.uint8)
+            check(lib().welvet_hip_dense_mount_native(
+                batch, self.inn, self.out, act, dtype, raw.ctypes.data_as(_u8), raw.size,
+                float(native[1]), _dp(b), 0 if b is None else b.size, C.byref(h)))
         self.h = h
 
     def close(self):
-        if self.h:
+        if getattr(self, "h", None):
             lib().welvet_dense_release(self.h)
             self.h = None
 
