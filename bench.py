@@ -19,9 +19,16 @@ roofline.traffic comes from the committed rocprofv3 --pmc passes
 (profiles/hbm_traffic.json); it is not measured live.
 
 cpu_baseline: the oracle's scalar port of the reference host path (per-element
-decode switch + f64 dot, oracle/oracle.c or_dense_forward_native), one thread,
-on the same workload for a bounded number of full steps; an all-core OpenMP
-run of the same port is reported beside it.
+decode switch + f64 dot, oracle/oracle.c or_dense_forward_native) on full
+FP8 and NF4 batch-1 steps, the median of 15 after a warm-up, one thread; an
+all-core OpenMP run of the same port and the host CPU model are reported
+beside it.
+
+Batched cases: roofline_frac is the executed MFMA rate against that
+instruction's dense peak (the split-x GEMM runs 3 bf16 products per fp32
+product, 6 for NF4, against the 2.5 PFLOP/s bf16 peak); the fp32-equivalent
+rate is reported beside it.  Configs 2-3 are timed as the median of 5
+repeats of at least 20 ms of back-to-back steps each.
 """
 from __future__ import annotations
 
@@ -102,9 +109,24 @@ def run_case(torch, pywelvet, dtype: int, batch: int, steps: int, warmup: int, s
     return r
 
 
-def cpu_baseline(dtype: int, batch: int, seconds: float = 12.0):
-    """Oracle scalar port on full 4096x11008 steps, bounded time: one thread
-    (the baseline), then every host core the run may use (reported beside)."""
+def cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo, as lscpu reports it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(dtypes=(4, 26), batch: int = 1, runs: int = 15):
+    """Oracle scalar port of the reference host path (per-element decode
+    switch + f64 dot) on full 4096x11008 batch-1 steps: one warm-up, then the
+    median of `runs` timed steps on one thread (the baseline) and on every
+    host core the run may use (reported beside).  The first dtype is the
+    headline's."""
     import numpy as np
     from oracle import Oracle
 
@@ -112,27 +134,37 @@ def cpu_baseline(dtype: int, batch: int, seconds: float = 12.0):
     rng = np.random.default_rng(0x5EED0002)
     W = rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02)
     x = rng.standard_normal((batch, IN), dtype=np.float32)
-    raw, scale = O.pack(dtype, W)
+    ncores = min(16, len(os.sched_getaffinity(0)))  # the GPU box grants 16 host threads
 
-    def timed(threads, budget):
-        steps, t = 0, 0.0
-        while t < budget and steps < 200:
+    def median_ms(dtype, raw, scale, threads):
+        O.forward_native(dtype, raw, scale, x, OUT, IN, -1, threads=threads)  # warm-up
+        t = []
+        for _ in range(runs):
             t0 = time.perf_counter()
             O.forward_native(dtype, raw, scale, x, OUT, IN, -1, threads=threads)
-            t += time.perf_counter() - t0
-            steps += 1
-        return steps, t, t / steps
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        return t[len(t) // 2] * 1e3, t
 
-    steps, t, per = timed(1, seconds)
-    ncores = min(16, len(os.sched_getaffinity(0)))  # the GPU box grants 16 host threads
-    msteps, mt, mper = timed(ncores, seconds / 3)
-    return {"value": packed_bytes(dtype) / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{steps} full steps of {pywelvet_name(dtype)} 4096x11008 b{batch} "
-                      f"({t:.1f} s): per-element decode switch + f64 dot, 1 thread",
-            "ms_per_step": per * 1e3,
-            "all_cores": {"value": packed_bytes(dtype) / mper / 1e9, "unit": "GB/s",
-                          "cores": ncores, "ms_per_step": mper * 1e3,
-                          "sample": f"{msteps} full steps ({mt:.1f} s), OpenMP over rows"}}
+    per = {}
+    total = 0.0
+    for dtype in dtypes:
+        raw, scale = O.pack(dtype, W)
+        ms1, t1 = median_ms(dtype, raw, scale, 1)
+        msn, tn = median_ms(dtype, raw, scale, ncores)
+        total += sum(t1) + sum(tn)
+        per[pywelvet_name(dtype)] = {
+            "gbs": packed_bytes(dtype) / (ms1 * 1e-3) / 1e9, "ms_per_step": ms1,
+            "all_cores": {"gbs": packed_bytes(dtype) / (msn * 1e-3) / 1e9, "ms_per_step": msn,
+                          "cores": ncores}}
+    head = per[pywelvet_name(dtypes[0])]
+    return {"value": head["gbs"], "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"median of {runs} full {pywelvet_name(dtypes[0])} 4096x11008 b{batch} "
+                      f"forward steps after one warm-up ({total:.1f} s of CPU work over all "
+                      f"legs): per-element decode switch + f64 dot, 1 thread",
+            "ms_per_step": head["ms_per_step"], "cpu_model": cpu_model(), "per_dtype": per,
+            "all_cores": {**head["all_cores"], "unit": "GB/s", "value": head["all_cores"]["gbs"],
+                          "sample": "same steps, OpenMP over output rows"}}
 
 
 # ---------------------------------------------------------------- configs
@@ -165,9 +197,30 @@ def _grid(P, widths, dtype, batch, rng, init, act_hidden=-1, act_out=-1, shared=
     return g
 
 
+def timed_repeats(torch, stream, step, est_ms, min_ms=20.0, repeats=5, min_steps=50):
+    """Median-of-repeats timing: each repeat runs enough back-to-back steps to
+    cover at least `min_ms` of GPU work (HIP events on the launch stream)."""
+    n = max(min_steps, int(min_ms / max(est_ms, 1e-4)) + 1)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per = []
+    i = 0
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(n):
+            step(i)
+            i += 1
+        t1.record(stream)
+        torch.cuda.synchronize()
+        per.append(t0.elapsed_time(t1) / n)
+    per.sort()
+    return {"ms_per_step": per[len(per) // 2], "ms_min": per[0], "ms_repeats": per,
+            "steps_per_repeat": n, "repeats": repeats}
+
+
 def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, init="normal"):
     """Forward of a Dense chain on device buffers; rotates grid copies so the
-    working set exceeds the MALL."""
+    working set exceeds the MALL.  Median of 5 repeats of >= 20 ms each."""
     import numpy as np
     rng = np.random.default_rng(seed)
     bits = P.dtype_bits(dtype)
@@ -185,21 +238,20 @@ def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, ini
         P.check(P.lib().welvet_hip_volume_forward_device(
             grids[i % copies].h, x.data_ptr(), widths[0], y.data_ptr(), widths[-1], sh))
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for i in range(steps):
+    for i in range(warmup):
         step(i)
     t1.record(stream)
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
+    est = t0.elapsed_time(t1) / max(1, warmup)
+    r = timed_repeats(torch, stream, step, est, min_steps=steps)
+    ms = r["ms_per_step"]
     for g in grids:
         g.close()
     flops = 2.0 * batch * sum(widths[i] * widths[i + 1] for i in range(len(widths) - 1))
     return {"widths": widths, "weight_dtype": P.DTYPE_NAMES[dtype], "batch": batch, "init": init,
-            "packed_bytes": wbytes, "weight_copies": copies, "ms_per_step": ms,
+            "packed_bytes": wbytes, "weight_copies": copies, **r,
             "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
@@ -224,21 +276,19 @@ def time_swiglu_forward(torch, P, inn, inter, dtype, batch, steps, warmup, seed)
     def step(i):
         P.check(layers[i % copies].forward_device(x.data_ptr(), h.data_ptr(), y.data_ptr(), sh))
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for i in range(steps):
+    for i in range(warmup):
         step(i)
     t1.record(stream)
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
+    r = timed_repeats(torch, stream, step, t0.elapsed_time(t1) / max(1, warmup), min_steps=steps)
+    ms = r["ms_per_step"]
     for L in layers:
         L.close()
     flops = 2.0 * batch * 3 * inn * inter
     return {"shape": [inn, inter], "weight_dtype": P.DTYPE_NAMES[dtype], "batch": batch,
-            "packed_bytes": wbytes, "weight_copies": copies, "ms_per_step": ms,
+            "packed_bytes": wbytes, "weight_copies": copies, **r,
             "hbm_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
@@ -286,9 +336,14 @@ def time_volume_train(torch, P, dims, widths, dtype, batch, steps, seed, lr=1e-3
     ms = (time.perf_counter() - t0) * 1e3 / steps
     g.close()
     mac = sum(widths[i] * widths[i + 1] for i in range(len(widths) - 1))
+    # executed: forward, dX and dW of every layer (2 flops per MAC each),
+    # except the first layer's dX, which the step never computes (its input
+    # gradient is not returned)
+    flops = 6.0 * batch * mac - 2.0 * batch * widths[0] * widths[1]
     return {"widths": widths if len(widths) < 8 else f"{len(widths) - 1} x {widths[1]}",
             "weight_dtype": P.DTYPE_NAMES[dtype], "batch": batch, "steps": steps, "lr": lr,
-            "ms_per_step": ms, "tflops": 6.0 * batch * mac / (ms * 1e-3) / 1e12,
+            "ms_per_step": ms, "gflop_per_step": flops / 1e9,
+            "tflops": flops / (ms * 1e-3) / 1e12,
             "loss_first": first_loss, "loss_last": loss.value,
             "sgd_skipped_nonfinite": sum(1 for c in codes if c)}
 
@@ -436,6 +491,8 @@ def main():
         print(f"# {name}: {results[name]['hbm_gbs']:.1f} GB/s  {results[name]['tflops']:.2f} TFLOP/s"
               f"  {results[name]['ms_per_step'] * 1e3:.2f} us/step", file=sys.stderr, flush=True)
     prim = results.get("fp8b1") or next(iter(results.values()))
+    for r in results.values():
+        annotate_roofline(r)
     # One step of a batch-1 case is exactly one GEMV launch, so the timed
     # region's mean step time is that kernel's mean launch duration.
     if prim["batch"] == 1:
@@ -443,21 +500,11 @@ def main():
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK, "unit": "GB/s",
                 "frac": ach / HBM_PEAK, "traffic": measured_traffic(prim_name(results, prim))}
     else:
-        ach = prim["tflops"]
-        roof = {"bound": "mfma", "achieved": ach, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-                "frac": ach / FP32_MFMA_PEAK, "traffic": measured_traffic(prim_name(results, prim))}
-    for r in results.values():
-        r["roofline_frac"] = (r["hbm_gbs"] / HBM_PEAK if r["batch"] == 1
-                              else r["tflops"] / FP32_MFMA_PEAK)
-        if r["batch"] > 4 and r["weight_dtype"] in SPLIT_X_DTYPES:
-            # the split-x GEMM runs the fp32 product as exact bf16 MFMA
-            # products: 3 per product (6 for NF4, whose table values are split
-            # too); executed bf16 flops against the bf16 peak
-            r["gemm"] = "split-x bf16 MFMA (x = hi + mid + lo exactly; fp32 accumulate)"
-            r["bf16_mfma_frac"] = (6 if r["weight_dtype"] == "nf4" else 3) * r["tflops"] / BF16_MFMA_PEAK
-            r["hbm_frac"] = r["hbm_gbs"] / HBM_PEAK
-        elif r["batch"] > 4:
-            r["gemm"] = "fp32 MFMA (v_mfma_f32_32x32x2f32)"
+        roof = {"bound": "mfma", "achieved": prim["executed_tflops"], "peak": prim["peak_tflops"],
+                "unit": "TFLOP/s", "frac": prim["roofline_frac"],
+                "traffic": measured_traffic(prim_name(results, prim)),
+                "fp32_equivalent": {"achieved": prim["tflops"], "peak": FP32_MFMA_PEAK,
+                                    "frac": prim["tflops"] / FP32_MFMA_PEAK}}
     line = {
         "metric": METRIC, "value": prim["hbm_gbs"] if prim["batch"] == 1 else prim["tflops"],
         "unit": "GB/s" if prim["batch"] == 1 else "TFLOP/s", "n_gpus": 1, "steps": a.steps,
@@ -474,8 +521,37 @@ def main():
     if not a.no_configs:
         line["config_results"] = run_configs(torch, pywelvet, tuple(a.configs.split(",")))
     if not a.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(prim["weight_dtype"] == "nf4" and 26 or 4, prim["batch"])
+        first = 26 if prim["weight_dtype"] == "nf4" else 4
+        line["cpu_baseline"] = cpu_baseline((first, 30 - first), prim["batch"])
     print(json.dumps(line), flush=True)
+
+
+def annotate_roofline(r):
+    """Roofline fraction of one case.  Batch 1: packed-weight bytes against the
+    HBM peak.  Batched: the flops the MFMA pipe executes against that
+    instruction's dense peak.  The split-x GEMM (FP8, Int8, FP4, NF4 weights)
+    forms each fp32 product from exact bf16 products, 3 per product (x split
+    into three parts), 6 for NF4 (its table values are split too), on the
+    bf16 MFMA; other formats run the fp32 MFMA.  The fp32-equivalent rate
+    (2*B*K*N / time) is kept beside it."""
+    r["hbm_frac"] = r["hbm_gbs"] / HBM_PEAK
+    if r["batch"] <= 4:
+        r["roofline_frac"] = r["hbm_frac"]
+        r["bound"] = "hbm"
+        return
+    r["bound"] = "mfma"
+    if r["weight_dtype"] in SPLIT_X_DTYPES:
+        mult = 6 if r["weight_dtype"] == "nf4" else 3
+        r["gemm"] = (f"split-x bf16 MFMA: x = hi + mid + lo exactly, {mult} exact bf16 products "
+                     f"per fp32 product, fp32 accumulate")
+        r["executed_tflops"] = mult * r["tflops"]
+        r["peak_tflops"] = BF16_MFMA_PEAK
+    else:
+        r["gemm"] = "fp32 MFMA (v_mfma_f32_32x32x2f32)"
+        r["executed_tflops"] = r["tflops"]
+        r["peak_tflops"] = FP32_MFMA_PEAK
+    r["roofline_frac"] = r["executed_tflops"] / r["peak_tflops"]
+    r["fp32_equivalent_frac"] = r["tflops"] / FP32_MFMA_PEAK
 
 
 def prim_name(results, prim):
