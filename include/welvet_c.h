@@ -182,10 +182,30 @@ WELVET_API welvet_status welvet_hip_dense_mount_native(int32_t batch, int32_t in
                                                        welvet_dense_session **sess);
 
 /* Forward on device pointers (16-byte aligned) enqueued on `stream`
- * (a hipStream_t; NULL = the HIP null stream); returns once enqueued. */
+ * (a hipStream_t; NULL = the HIP null stream); returns once enqueued.
+ * The launch uses the session's own workspace (stream-K partial tiles), so
+ * calls on one session must not overlap: forwards on one stream are ordered
+ * by that stream; before a call on the same session from another stream,
+ * or a host-buffer call (execute, backward, sgd, export, native: these run
+ * on the session's internal stream and return when done), synchronise
+ * `stream`.  Sessions are independent of each other. */
 WELVET_API welvet_status welvet_hip_dense_forward_device(welvet_dense_session *s, const float *d_x,
                                                          float *d_pre, float *d_post,
                                                          void *stream);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): welvet_hip_dense_forward_device for `batch` rows
+ * (any batch >= 1, independent of the mount's) that allocates nothing.  Its
+ * stream-K partial tiles live in one library-wide 64 MiB device array per
+ * GPU, held until the process ends, instead of the session's workspace; code
+ * 1 when the batch's plan needs more than 64 MiB (4096 x 11008 weights:
+ * batch 64 needs 60 MB).  Every call on one GPU shares that array, whatever
+ * the session or stream: calls that overlap on one GPU race, so order them
+ * on one stream or synchronise between them.  Enqueued on `stream`; returns
+ * once enqueued. */
+WELVET_API welvet_status welvet_hip_dense_forward_noalloc(welvet_dense_session *s, int32_t batch,
+                                                          const float *d_x, float *d_pre,
+                                                          float *d_post, void *stream);
 /* The store in the reference's byte layout (WeightStore::native, with the
  * 4-byte min header of the unsigned types; f32 bytes for Float32).  *len gets
  * the payload size; fails with code 1 when cap is too small. */
@@ -234,7 +254,11 @@ WELVET_API welvet_status welvet_hip_grid_set_disabled(welvet_hip_grid *g, int32_
  * (grid.cpp:82-95): x [batch*in] -> y [batch*out], out = the last hop's width. */
 WELVET_API welvet_status welvet_hip_volume_forward(welvet_hip_grid *g, const float *x, int32_t in,
                                                    float *y, int32_t out);
-/* The same on device pointers, enqueued on `stream` (NULL = null stream). */
+/* The same on device pointers, enqueued on `stream` (NULL = null stream);
+ * returns once enqueued.  The cells' activation buffers and workspace belong
+ * to the grid: calls on one grid must not overlap (synchronise `stream`
+ * before a call on the same grid from another stream or a host-buffer
+ * call). */
 WELVET_API welvet_status welvet_hip_volume_forward_device(welvet_hip_grid *g, const float *d_x,
                                                           int32_t in, float *d_y, int32_t out,
                                                           void *stream);

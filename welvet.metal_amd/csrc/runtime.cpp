@@ -369,6 +369,41 @@ welvet_status forward_device(welvet_dense_session *s, const float *x, float *pre
   return ok();
 }
 
+// ------------------------------------------------- no-allocation forward
+// The stream-K partial tiles of welvet_hip_dense_forward_noalloc live in this
+// file-scope device array instead of a session workspace, so that call
+// allocates nothing.  Every GPU the library runs on holds its own copy for the
+// life of the process; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (the array's name on the
+// host is a stand-in, not a device address).  Every slot a reduce reads is
+// written by the same launch's GEMM first, so nothing needs clearing.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+struct ScratchAddr {
+  std::once_flag once;
+  void *ptr = nullptr;
+  hipError_t err = hipErrorNotInitialized;
+};
+ScratchAddr g_scratch[kMaxDevices];
+
+// The current device's copy of `scratch`, looked up once per device (with
+// that device current); null when the lookup failed.
+void *scratch_ptr(hipError_t *err) {
+  int dev = -1;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  ScratchAddr &a = g_scratch[dev];
+  std::call_once(a.once, [&a] { a.err = hipGetSymbolAddress(&a.ptr, HIP_SYMBOL(scratch)); });
+  *err = a.err;
+  return a.err == hipSuccess ? a.ptr : nullptr;
+}
+
 // Where a mount's weights come from: f32 values on the host or the device
 // (encoded on the device), or a store snapshot in the reference's native
 // byte layout (taken byte for byte).
@@ -623,6 +658,28 @@ welvet_status welvet_hip_dense_forward_device(welvet_dense_session *s, const flo
     return make_status(kInvalid, "device pointers must be 16-byte aligned");
   std::lock_guard<std::mutex> lock(s->mu);
   return forward_device(s, d_x, d_pre, d_post, (hipStream_t)stream);
+}
+
+welvet_status welvet_hip_dense_forward_noalloc(welvet_dense_session *s, int32_t batch,
+                                               const float *d_x, float *d_pre, float *d_post,
+                                               void *stream) {
+  if (!s || !d_x || !d_pre || !d_post) return make_status(kInvalid, "null execute args");
+  if (((uintptr_t)d_x | (uintptr_t)d_pre | (uintptr_t)d_post) & 15)
+    return make_status(kInvalid, "device pointers must be 16-byte aligned");
+  if (batch <= 0) return make_status(kInvalid, "bad batch %d", batch);
+  const size_t need = forward_workspace_bytes(s->W.dev(), batch);
+  if (need > kScratchBytes)
+    return make_status(kInvalid, "no-allocation forward: batch %d needs %zu bytes of scratch (limit %zu)",
+                       batch, need, kScratchBytes);
+  WH_HIP(hipSetDevice(g_dev.id));
+  hipError_t e = hipSuccess;
+  void *ws = scratch_ptr(&e);
+  if (ws == nullptr)
+    return make_status(kInternal, "no-allocation forward: scratch address: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(s->mu);
+  WH_HIP(launch_forward(s->W.dev(), batch, d_x, s->W.bias, s->W.bias_len, s->act, d_pre, d_post, ws,
+                        kScratchBytes, (hipStream_t)stream));
+  return ok();
 }
 
 welvet_status welvet_hip_dense_native(welvet_dense_session *s, uint8_t *out, size_t cap,

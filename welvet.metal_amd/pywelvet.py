@@ -139,6 +139,8 @@ def lib() -> C.CDLL:
         L.welvet_hip_dense_mount_native.restype = Status
         L.welvet_hip_dense_forward_device.argtypes = [_vp, _vp, _vp, _vp, _vp]
         L.welvet_hip_dense_forward_device.restype = Status
+        L.welvet_hip_dense_forward_noalloc.argtypes = [_vp, _i32, _vp, _vp, _vp, _vp]
+        L.welvet_hip_dense_forward_noalloc.restype = Status
         L.welvet_hip_dense_native.argtypes = [_vp, _u8, C.c_size_t, C.POINTER(C.c_size_t), _f]
         L.welvet_hip_dense_native.restype = Status
         L.welvet_hip_dense_export_f32.argtypes = [_vp, _f]
@@ -470,6 +472,13 @@ class Session:
 
     def forward_device(self, d_x: int, d_pre: int, d_post: int, stream: int | None = None):
         check(lib().welvet_hip_dense_forward_device(self.h, d_x, d_pre, d_post, stream))
+
+    def forward_noalloc(self, batch: int, d_x: int, d_pre: int, d_post: int,
+                        stream: int | None = None, status: bool = False):
+        st = lib().welvet_hip_dense_forward_noalloc(self.h, batch, d_x, d_pre, d_post, stream)
+        if status:
+            return st
+        check(st)
 
     def native(self):
         n = C.c_size_t()
