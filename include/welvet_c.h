@@ -211,6 +211,15 @@ WELVET_API welvet_status welvet_hip_dense_forward_noalloc(welvet_dense_session *
  * the payload size; fails with code 1 when cap is too small. */
 WELVET_API welvet_status welvet_hip_dense_native(welvet_dense_session *s, uint8_t *out,
                                                  size_t cap, size_t *len, float *scale);
+/* WeightStore::set_from_f32_gpu (reference src/weights/native_codec.cpp:
+ * 872-907, kernel shaders/ops_storage.metal:971-1144 op_native_repack): the
+ * resident store replaced by `values` [out*in] re-encoded in its dtype with
+ * fresh statistics (a new scale, and min for the unsigned types); Float32
+ * takes the values as they are.  Code 1 "blend: invalid native store
+ * replacement" when len != out*in (or 0).  The reference calls it for
+ * CamSync's blended weights (src/systems/cam_sync.cpp:148). */
+WELVET_API welvet_status welvet_hip_dense_repack(welvet_dense_session *s, const float *values,
+                                                 size_t len);
 /* WeightStore::export_f32 of the resident store into W_out [out*in]. */
 WELVET_API welvet_status welvet_hip_dense_export_f32(welvet_dense_session *s, float *W_out);
 /* Backward against the resident weights (host pointers): x [batch*in], pre and
@@ -286,6 +295,10 @@ WELVET_API welvet_status welvet_hip_volume_train_step_device(welvet_hip_grid *g,
 /* WeightStore::export_f32 / native bytes of one bound cell. */
 WELVET_API welvet_status welvet_hip_grid_export_f32(welvet_hip_grid *g, int32_t z, int32_t y,
                                                     int32_t x, int32_t l, float *W_out);
+/* welvet_hip_dense_repack of one bound cell's store. */
+WELVET_API welvet_status welvet_hip_grid_repack(welvet_hip_grid *g, int32_t z, int32_t y,
+                                                int32_t x, int32_t l, const float *values,
+                                                size_t len);
 WELVET_API welvet_status welvet_hip_grid_native(welvet_hip_grid *g, int32_t z, int32_t y,
                                                 int32_t x, int32_t l, uint8_t *out, size_t cap,
                                                 size_t *len, float *scale);

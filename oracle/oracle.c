@@ -771,6 +771,167 @@ int or_native_sgd(int dt, uint8_t *raw, int64_t raw_n, float scale, int64_t n, c
   return 0;
 }
 
+/* op_native_repack ops_storage.metal:971-1144 (the complete store
+ * replacement behind WeightStore::set_from_f32_gpu, native_codec.cpp:872-907):
+ * fresh statistics and scale, then every element re-encoded.
+ *  - statistics: hi = max |a[i]|, mn / mx = min / max of a[i]; Metal's
+ *    max/min return the other operand of a NaN, so NaN elements (element 0
+ *    included) are skipped; with no number at all mn = mx = NaN.  Equal
+ *    extremes keep the first element that attains them (the sign of a zero
+ *    extreme is where Metal's min/max leave the choice open).
+ *  - cam_div / cam_mul divide / multiply through double-float and round to
+ *    f32: for two f32 operands that is the correctly rounded f32 quotient /
+ *    product (the f64 result holds it exactly, or rounds innocuously), so
+ *    they are f32 '/' and '*' here.
+ *  - scale: base = hi (0 -> 1); Int64 / Int base / 1e6, Int32 base /
+ *    2147483647 (= 2^31 as float), Int16 base / 32767, Int8 hi / 127 (0 -> 1),
+ *    Int4 hi / 7 (0 -> 1), Int2 / Ternary / Binary / NF4 base, n-bit signed
+ *    hi / (2^(bits-1) - 1) (0 -> 1), unsigned span / maxu with the f32 min
+ *    as the 4-byte header; every other dtype 1.
+ *  - codes as pack_native's, except Uint2 (q = round(fl32(fl32((v - mn) /
+ *    span) * 3.0f)), an f32 multiply where pack rounds a double product) and
+ *    the unsigned qf clamped below by max(0, qf) (NaN -> 0); the float
+ *    formats, Binary and the complex types go through set_weight_at with
+ *    the new scale (or_set).
+ * Returns 0, or 1 for bad arguments. */
+int or_repack(int dt, const float *a, int64_t n, uint8_t *raw, int64_t raw_n, float *scale_out) {
+  if (n <= 0 || dt < 0 || dt >= OR_NUM_DTYPES) return 1;
+  const int64_t bytes = or_native_bytes(dt, n);
+  if (bytes < 0 || raw_n < bytes) return 1;
+  memset(raw, 0, (size_t)bytes);
+  float hi = 0, mn = NAN, mx = NAN;
+  int have = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = a[i];
+    if (fabsf(v) > hi) hi = fabsf(v);
+    if (v != v) continue;
+    if (!have) {
+      mn = mx = v;
+      have = 1;
+    } else {
+      if (v < mn) mn = v;
+      if (v > mx) mx = v;
+    }
+  }
+  const float base = hi == 0 ? 1 : hi;
+  float span = mx - mn;
+  if (span == 0) span = 1;
+  float scale = 1;
+  const int uns = dt == OR_UINT64 || dt == OR_UINT32 || dt == OR_UINT16 || dt == OR_UINT8 ||
+                  dt == OR_UINT4 || dt == OR_UINT2 || dt == OR_UINT || dt == OR_UINTPTR ||
+                  dt == OR_UINT6 || dt == OR_UINT5 || dt == OR_UINT3;
+  const int nbit = dt == OR_FP6 || dt == OR_INT6 ? 6 : dt == OR_INT5 ? 5 : dt == OR_INT3 ? 3 : 0;
+  if (dt == OR_INT64 || dt == OR_INT) scale = base / 1e6f;
+  if (dt == OR_INT32) scale = base / 2147483647.0f;
+  if (dt == OR_INT16) scale = base / 32767.0f;
+  if (dt == OR_INT8) {
+    scale = hi / 127.0f;
+    if (scale == 0) scale = 1;
+  }
+  if (dt == OR_INT4) {
+    scale = hi / 7.0f;
+    if (scale == 0) scale = 1;
+  }
+  if (dt == OR_INT2 || dt == OR_TERNARY || dt == OR_BINARY || dt == OR_NF4) scale = base;
+  if (nbit) {
+    scale = hi / (float)((1 << (nbit - 1)) - 1);
+    if (scale == 0) scale = 1;
+  }
+  float maxu = 1;
+  if (uns) {
+    maxu = (dt == OR_UINT64 || dt == OR_UINT || dt == OR_UINTPTR) ? 1e15f
+           : dt == OR_UINT32 ? 4294967295.0f
+           : dt == OR_UINT16 ? 65535.0f
+           : dt == OR_UINT8 ? 255.0f
+           : dt == OR_UINT4 ? 15.0f
+           : dt == OR_UINT2 ? 3.0f
+           : (float)((1 << (dt == OR_UINT6 ? 6 : dt == OR_UINT5 ? 5 : 3)) - 1);
+    scale = span / maxu;
+    put_u32(raw, 0, f32bits(mn));
+  }
+  *scale_out = scale;
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = a[i];
+    switch (dt) {
+    case OR_FLOAT32: put_u32(raw, i * 4, f32bits(v)); continue;
+    case OR_FLOAT64: put_u64(raw, i * 8, f64bits((double)v)); continue;
+    case OR_INT64: case OR_INT:
+      put_u64(raw, i * 8, (uint64_t)cvt_i64(roundf(v / base * 1e6f)));
+      continue;
+    case OR_INT32: {
+      int64_t q = cvt_i64(roundf(v / base * 2147483647.0f));
+      q = q < -2147483648LL ? -2147483648LL : (q > 2147483647LL ? 2147483647LL : q);
+      put_u32(raw, i * 4, (uint32_t)q);
+      continue;
+    }
+    case OR_INT16: put_u16(raw, i * 2, (uint16_t)cvt_i64(roundf(v / base * 32767.0f))); continue;
+    case OR_INT8: {
+      int64_t q = cvt_i64(roundf(v / scale));
+      q = q < -128 ? -128 : (q > 127 ? 127 : q);
+      raw[i] = (uint8_t)q;
+      continue;
+    }
+    case OR_INT4: {
+      int q = cvt_i32(roundf(v / scale));
+      q = q < -8 ? -8 : (q > 7 ? 7 : q);
+      put_nibble(raw, i, (uint8_t)(q & 15));
+      continue;
+    }
+    case OR_INT2: {
+      int q = cvt_i32(roundf(v / scale));
+      q = q < -2 ? -2 : (q > 1 ? 1 : q);
+      put_2bit(raw, i, (uint8_t)((q + 2) & 3));
+      continue;
+    }
+    case OR_TERNARY: {
+      const float norm = v / scale;
+      put_2bit(raw, i, norm > .5f ? 2 : norm < -.5f ? 0 : 1);
+      continue;
+    }
+    case OR_NF4: {
+      const float norm = v / scale;
+      float err = FLT_MAX;
+      int best = 0;
+      for (int c = 0; c < 16; ++c) {
+        const float d = fabsf(norm - kNf4[c]);
+        if (d < err) {
+          err = d;
+          best = c;
+        }
+      }
+      put_nibble(raw, i, (uint8_t)best);
+      continue;
+    }
+    case OR_FP6: case OR_INT6: case OR_INT5: case OR_INT3: {
+      const int lim = 1 << (nbit - 1);
+      int q = cvt_i32(roundf(v / scale));
+      q = q < -lim ? -lim : (q > lim - 1 ? lim - 1 : q);
+      put_bits(raw, i, nbit, (uint64_t)((uint32_t)q & ((1u << nbit) - 1)));
+      continue;
+    }
+    default: break;
+    }
+    if (uns) {
+      float qf = roundf((v - mn) / span * maxu);
+      qf = fmaxf(0.0f, qf);  /* Metal max: NaN -> 0 */
+      uint64_t q = cvt_u64(qf);
+      if (dt == OR_UINT32 && q > 4294967295ull) q = 4294967295ull;
+      uint8_t *body = raw + 4;
+      if (dt == OR_UINT64 || dt == OR_UINT || dt == OR_UINTPTR) put_u64(body, i * 8, q);
+      else if (dt == OR_UINT32) put_u32(body, i * 4, (uint32_t)q);
+      else if (dt == OR_UINT16) put_u16(body, i * 2, (uint16_t)q);
+      else if (dt == OR_UINT8) body[i] = (uint8_t)q;
+      else if (dt == OR_UINT4) put_nibble(body, i, (uint8_t)q);
+      else if (dt == OR_UINT2) put_2bit(body, i, (uint8_t)q);
+      else put_bits(body, i, dt == OR_UINT6 ? 6 : dt == OR_UINT5 ? 5 : 3, q);
+      continue;
+    }
+    /* Float16, BFloat16, FP8, FP4, Binary, Complex64/128: set_weight_at */
+    if (or_set(dt, raw, raw_n, scale, i, n, v)) return 1;
+  }
+  return 0;
+}
+
 /* welvet_sgd_f32_f64_grad welvet_dense.metal:263-281: the step is rounded to
  * f32 first, then subtracted in f32. */
 void or_sgd_f32(float *w, const float *dW, int64_t n, double lr) {

@@ -104,6 +104,7 @@ int or_normalbp(int batch, int in, int out, int act, int dtype, const float *W_i
                 int use_target, double lr, float *pre, float *post, float *dX, float *dW,
                 float *W_after, double *loss);
 
+int or_repack(int dt, const float *a, int64_t n, uint8_t *raw, int64_t raw_n, float *scale_out);
 void or_decode_many(int kind, const uint32_t *codes, int64_t n, float *out);
 void or_encode_many(int kind, const float *in, int64_t n, void *out);
 

@@ -90,6 +90,8 @@ class Oracle:
         L.or_encode_many.restype = None
         L.or_decode_many.argtypes = [_i, _vp, _i64, _vp]
         L.or_decode_many.restype = None
+        L.or_repack.argtypes = [_i, _vp, _i64, _vp, _i64, C.POINTER(_f)]
+        L.or_repack.restype = _i
         L.or_swiglu_h.argtypes = [_vp, _vp, _i64, _vp]
         L.or_swiglu_h.restype = None
         L.or_swiglu_split.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp]
@@ -141,6 +143,16 @@ class Oracle:
         out = np.zeros(x.size, np.uint16 if kind in (0, 1) else np.uint8)
         self.lib.or_encode_many(kind, _ptr(x), x.size, _ptr(out))
         return out
+
+    def repack(self, dtype: int, w: np.ndarray) -> tuple[np.ndarray, float]:
+        """op_native_repack: fresh statistics and scale, every element re-encoded."""
+        w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+        out = np.zeros(self.native_bytes(dtype, w.size), np.uint8)
+        s = _f()
+        st = self.lib.or_repack(dtype, _ptr(w), w.size, _ptr(out), out.size, C.byref(s))
+        if st:
+            raise ValueError(f"or_repack status {st}")
+        return out, s.value
 
     def decode_many(self, kind: int, codes) -> np.ndarray:
         """Scalar-codec decode of every code (kind 0 f16, 1 bf16, 2 e4m3,

@@ -124,7 +124,53 @@ __global__ void finalize_kernel(const float *__restrict__ w, const Stats *acc, M
   *meta = m;
 }
 
+// The statistics of op_native_repack ops_storage.metal:983-1024: Metal's
+// max / min return the other operand of a NaN, so NaN elements (element 0
+// included) never become the min or max; with no number at all min = max =
+// NaN.  Scale rules as pack's (the same divisors; Int8 / Int4 / n-bit use the
+// absmax, 0 -> 1).
 template <int DT>
+__global__ void repack_finalize_kernel(const float *__restrict__ w, const Stats *acc, Meta *meta) {
+  const float absmax = u2f(acc->absmax_bits);
+  float mn = __builtin_nanf(""), mx = mn;
+  if (acc->minkey != ~0ull) {
+    mn = w[(uint32_t)acc->minkey];
+    mx = w[0xffffffffu - (uint32_t)acc->maxkey];
+  }
+  Meta m{1.0f, 1.0f, 0.0f, 0.0f};
+  if constexpr (DT == kInt64 || DT == kInt || DT == kInt32 || DT == kInt16) {
+    float s = absmax;
+    if (s == 0) s = 1;
+    m.s = s;
+    m.scale = s / (DT == kInt32 ? 2147483647.0f : (DT == kInt16 ? 32767.0f : 1e6f));
+  } else if constexpr (DT == kInt8 || DT == kInt4 || DT == kInt6 || DT == kFP6 || DT == kInt5 ||
+                       DT == kInt3) {
+    constexpr int bits = dtype_bits(DT);
+    float s = absmax / (float)((1 << (bits - 1)) - 1);
+    if (s == 0) s = 1;
+    m.s = m.scale = s;
+  } else if constexpr (DT == kInt2 || DT == kTernary || DT == kBinary || DT == kNF4) {
+    float s = absmax;
+    if (s == 0) s = 1;
+    m.s = m.scale = s;
+  } else if constexpr (dtype_has_min(DT)) {
+    float span = mx - mn;
+    if (span == 0) span = 1;
+    float k;
+    if constexpr (DT == kUint8) k = 255.0f;
+    else if constexpr (DT == kUint16) k = 65535.0f;
+    else if constexpr (DT == kUint32) k = 4294967296.0f;  // float(4294967295)
+    else if constexpr (DT == kUint2) k = 3.0f;
+    else if constexpr (DT == kUint64 || DT == kUint || DT == kUintptr) k = 1e15f;
+    else k = (float)((1 << dtype_bits(DT)) - 1);
+    m.s = span;
+    m.minv = mn;
+    m.scale = span / k;
+  }
+  *meta = m;
+}
+
+template <int DT, bool REPACK = false>
 __global__ void __launch_bounds__(kThreads) pack_kernel(const float *__restrict__ w, int64_t n,
                                                         uint8_t *__restrict__ body,
                                                         uint8_t *__restrict__ kbody,
@@ -136,7 +182,7 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const float *__restrict_
   for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < units;
        u += (int64_t)gridDim.x * kThreads) {
     if constexpr (bits >= 8) {
-      const uint64_t c = pack_code<DT>(w[u], m);
+      const uint64_t c = REPACK ? repack_code<DT>(w[u], m) : pack_code<DT>(w[u], m);
       if constexpr (has_kcopy<DT>()) kbody[u] = kcode<DT>((uint32_t)c);
       if constexpr (bits == 8) body[u] = (uint8_t)c;
       else if constexpr (bits == 16) ((uint16_t *)body)[u] = (uint16_t)c;
@@ -156,7 +202,7 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const float *__restrict_
 #pragma unroll
       for (int j = 0; j < U; ++j) {
         const int64_t i = u * U + j;
-        if (i < n) acc |= pack_code<DT>(w[i], m) << (j * bits);
+        if (i < n) acc |= (REPACK ? repack_code<DT>(w[i], m) : pack_code<DT>(w[i], m)) << (j * bits);
       }
       constexpr int ubytes = U * bits / 8;
 #pragma unroll
@@ -350,17 +396,23 @@ __global__ void __launch_bounds__(kThreads) e5m2_nonfinite_kernel(const uint8_t 
   }
 
 hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, uint8_t *kbody, Meta *meta,
-                         Stats *stats, hipStream_t s) {
+                         Stats *stats, hipStream_t s, bool repack) {
   if (n <= 0) return hipErrorInvalidValue;
   if ((dt == kFP8E4M3 || dt == kFP8E5M2) && kbody == nullptr) return hipErrorInvalidValue;
   stats_init_kernel<<<1, 1, 0, s>>>(stats);
   int sblocks = grid_for(n / 4 + 1);
   if (sblocks > 1024) sblocks = 1024;
   stats_kernel<<<sblocks, kThreads, 0, s>>>(w, n, stats);
-#define WH_ENC(D)                                                                      \
-  finalize_kernel<D><<<1, 1, 0, s>>>(w, stats, meta);                                  \
-  pack_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
-      w, n, body, kbody, meta);                                                        \
+#define WH_ENC(D)                                                                                  \
+  if (repack) {                                                                                    \
+    repack_finalize_kernel<D><<<1, 1, 0, s>>>(w, stats, meta);                                     \
+    pack_kernel<D, true><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
+        w, n, body, kbody, meta);                                                                  \
+  } else {                                                                                         \
+    finalize_kernel<D><<<1, 1, 0, s>>>(w, stats, meta);                                            \
+    pack_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>(     \
+        w, n, body, kbody, meta);                                                                  \
+  }                                                                                                \
   return hipGetLastError();
   WH_DTYPE_SWITCH(dt, WH_ENC)
 #undef WH_ENC

@@ -121,6 +121,23 @@ __device__ inline uint64_t pack_code(float w, const Meta &m) {
   }
 }
 
+// ----------------------------------------------------------------- repack
+// op_native_repack ops_storage.metal:971-1144 (WeightStore::set_from_f32_gpu):
+// the code of w under fresh statistics.  Its cam_div / cam_mul are the
+// correctly rounded f32 '/' and '*', so every dtype's code is pack_code's
+// except Uint2, whose product with 3 is an f32 multiply there
+// (round(fl32(fl32((w - min) / span) * 3.0f))) where pack rounds a double
+// product.  The statistics differ in their NaN rule (repack_finalize_kernel).
+template <int DT>
+__device__ inline uint64_t repack_code(float w, const Meta &m) {
+  if constexpr (DT == kUint2) {
+    const float qf = roundf((w - m.minv) / m.s * 3.0f);
+    return (uint32_t)sat_i32(clampf_(qf, 0.0f, 3.0f)) & 3u;
+  } else {
+    return pack_code<DT>(w, m);
+  }
+}
+
 // -------------------------------------------------------------- re-encode
 // set_weight_at ops_storage.metal:655-921: the code of v under the stored
 // scale and min.  The clamp bounds are float there, so the Int32 and Uint32

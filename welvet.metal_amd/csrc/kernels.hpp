@@ -36,8 +36,9 @@ struct DevStore {
 
 // ---- codec.hip
 // FP8 formats also write the decode-ready copy kbody (required for them).
+// repack: the statistics and codes of op_native_repack instead of pack_native.
 hipError_t launch_encode(int dt, const float *w, int64_t n, uint8_t *body, uint8_t *kbody, Meta *meta,
-                         Stats *stats, hipStream_t s);
+                         Stats *stats, hipStream_t s, bool repack = false);
 hipError_t launch_decode(int dt, const uint8_t *body, int64_t n, float scale, float minv, float *out,
                          hipStream_t s);
 hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s);

@@ -149,6 +149,17 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
     WH_HIP(hipMalloc(&w->kbody, alloc));
     WH_HIP(hipMemsetAsync(w->kbody, 0, alloc, s));
   }
+  return store_encode(w, d_w, false, s);
+}
+
+// Encodes f32 values already in HBM into the store's existing allocation:
+// pack_native's statistics and codes, or op_native_repack's (repack); then
+// the scale, min, decode tables and non-finite flag follow the new codes and
+// the transposed copy is stale.
+welvet_status store_encode(Store *w, const float *d_w, bool repack, hipStream_t s) {
+  const int dtype = w->dtype;
+  const int64_t n = w->n();
+  w->tbody_ok = false;
   if (dtype == kFloat32) {
     WH_HIP(hipMemcpyAsync(w->body, d_w, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
     w->scale = 1.0f;
@@ -157,7 +168,7 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
   }
   EncodeScratch *scratch = nullptr;
   WH_HIP(hipMalloc(&scratch, sizeof(EncodeScratch)));
-  hipError_t e = launch_encode(dtype, d_w, n, w->body, w->kbody, &scratch->meta, &scratch->stats, s);
+  hipError_t e = launch_encode(dtype, d_w, n, w->body, w->kbody, &scratch->meta, &scratch->stats, s, repack);
   Meta m{};
   int nonfinite = 0;
   if (dtype == kFP8E5M2) {
@@ -173,7 +184,7 @@ welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d
   w->minv = m.minv;
   w->finite = nonfinite == 0;
   if (dtype_lut(dtype)) {
-    WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
+    if (w->lut == nullptr) WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
     WH_HIP(launch_lut(dtype, w->scale, w->minv, w->lut, s));
     WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
     WH_HIP(hipStreamSynchronize(s));
@@ -233,6 +244,20 @@ welvet_status store_from_native(Store *w, int dtype, int rows, int cols, float s
     WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
   }
   WH_HIP(hipStreamSynchronize(s));  // k and the caller's buffers outlive the copies
+  return ok();
+}
+
+welvet_status store_repack_host(Store *w, const float *values, hipStream_t s) {
+  float *d = nullptr;
+  const size_t bytes = (size_t)w->n() * sizeof(float);
+  WH_HIP(hipMalloc(&d, bytes));
+  hipError_t e = hipMemcpyAsync(d, values, bytes, hipMemcpyHostToDevice, s);
+  welvet_status st = e == hipSuccess ? store_encode(w, d, true, s)
+                                     : make_status(kInternal, "hip: %s", hipGetErrorString(e));
+  e = hipStreamSynchronize(s);
+  (void)hipFree(d);
+  if (st.code) return st;
+  WH_HIP(e);
   return ok();
 }
 
@@ -691,6 +716,15 @@ welvet_status welvet_hip_dense_native(welvet_dense_session *s, uint8_t *out, siz
     if (scale) *scale = 1.0f;
   }
   return store_native(s->W, out, cap, len, s->stream);
+}
+
+welvet_status welvet_hip_dense_repack(welvet_dense_session *s, const float *values, size_t len) {
+  if (!s) return make_status(kInvalid, "null session");
+  if (!values || len == 0 || len != (size_t)s->W.n())
+    return make_status(kInvalid, "blend: invalid native store replacement");
+  std::lock_guard<std::mutex> lock(s->mu);
+  WH_HIP(hipSetDevice(g_dev.id));
+  return store_repack_host(&s->W, values, s->stream);
 }
 
 welvet_status welvet_hip_dense_export_f32(welvet_dense_session *s, float *W_out) {

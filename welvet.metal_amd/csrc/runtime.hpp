@@ -61,6 +61,12 @@ void free_store(Store *w);
 welvet_status store_prepare_backward(Store *w, int batch, hipStream_t s);
 // WeightStore::make on the device from f32 values already in HBM.
 welvet_status store_make(Store *w, int dtype, int rows, int cols, const float *d_w, hipStream_t s);
+// Re-encodes a made store from f32 values in HBM (pack_native, or the fresh
+// statistics and codes of op_native_repack when repack is set).
+welvet_status store_encode(Store *w, const float *d_w, bool repack, hipStream_t s);
+// WeightStore::set_from_f32_gpu (native_codec.cpp:872-907): the store
+// replaced by the op_native_repack encode of host values [rows*cols].
+welvet_status store_repack_host(Store *w, const float *values, hipStream_t s);
 welvet_status store_set_bias(Store *w, const double *bias, size_t bias_len, hipStream_t s);
 // A store from the fields of a WeightStore snapshot (model_session.cpp:128-151
 // read_store): Float32 takes the f32 payload, the other dtypes the native

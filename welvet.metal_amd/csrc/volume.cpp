@@ -589,6 +589,18 @@ welvet_status welvet_hip_grid_export_f32(welvet_hip_grid *g, int32_t z, int32_t 
   return ok();
 }
 
+welvet_status welvet_hip_grid_repack(welvet_hip_grid *g, int32_t z, int32_t y, int32_t x, int32_t l,
+                                     const float *values, size_t len) {
+  if (!g) return make_status(kInvalid, "invalid argument");
+  std::lock_guard<std::mutex> lk(g->mu);
+  Grid::Cell *c = nullptr;
+  welvet_status st = cell_at(g, z, y, x, l, &c);
+  if (st.code) return st;
+  if (!values || len == 0 || len != (size_t)c->W.n())
+    return make_status(kInvalid, "blend: invalid native store replacement");
+  return store_repack_host(&c->W, values, g->stream);
+}
+
 welvet_status welvet_hip_grid_native(welvet_hip_grid *g, int32_t z, int32_t y, int32_t x, int32_t l,
                                      uint8_t *out, size_t cap, size_t *len, float *scale) {
   if (!g) return make_status(kInvalid, "invalid argument");

@@ -143,6 +143,10 @@ def lib() -> C.CDLL:
         L.welvet_hip_dense_forward_noalloc.restype = Status
         L.welvet_hip_dense_native.argtypes = [_vp, _u8, C.c_size_t, C.POINTER(C.c_size_t), _f]
         L.welvet_hip_dense_native.restype = Status
+        L.welvet_hip_dense_repack.argtypes = [_vp, _f, C.c_size_t]
+        L.welvet_hip_dense_repack.restype = Status
+        L.welvet_hip_grid_repack.argtypes = [_vp] + [_i32] * 4 + [_f, C.c_size_t]
+        L.welvet_hip_grid_repack.restype = Status
         L.welvet_hip_dense_export_f32.argtypes = [_vp, _f]
         L.welvet_hip_dense_export_f32.restype = Status
         L.welvet_hip_dense_backward.argtypes = [_vp, _f, _f, _f, _f, _f]
@@ -494,6 +498,14 @@ class Session:
         check(lib().welvet_hip_dense_export_f32(self.h, _fp(out)))
         return out
 
+    def repack(self, values, status=False):
+        """WeightStore::set_from_f32_gpu: re-encode with fresh statistics."""
+        v = _f32(values).ravel()
+        st = lib().welvet_hip_dense_repack(self.h, _fp(v), v.size)
+        if status:
+            return st
+        check(st)
+
     def backward(self, x, pre, gy):
         x, pre, gy = _f32(x), _f32(pre), _f32(gy)
         dX = np.zeros((self.batch, self.inn), np.float32)
@@ -589,6 +601,13 @@ class Grid:
         W = np.zeros((out, inn), np.float32)
         check(lib().welvet_hip_grid_export_f32(self.h, *coord, _fp(W)))
         return W
+
+    def repack(self, coord, values, status=False):
+        v = _f32(values).ravel()
+        st = lib().welvet_hip_grid_repack(self.h, *coord, _fp(v), v.size)
+        if status:
+            return st
+        check(st)
 
     def native(self, coord):
         n = C.c_size_t()
