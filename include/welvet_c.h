@@ -341,14 +341,17 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2 and FP4, else 0) [-1]
  *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
  *     FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4 [1]
- *   11 its weight prefetch depth in k stages: 1, 2, or 3 (batch <= 32) [1]
+ *   11 its weight prefetch depth in k stages: 0 auto (1; 2 on the two-group
+ *      workgroups of key 15), 1, 2, or 3 (batch <= 32) [0]
  *   12 its block width: 0 = 256 output columns, 1 = 128 [0]
  *   13 dW kernel, every one bit-identical to the sequential FMA (the fp32
  *      MFMA accumulates each product with fmaf rounding, in k order): 2 MFMA
  *      with operands staged in LDS (out and in multiples of 128, else 1),
  *      1 MFMA with direct loads, 0 VALU [2]
  *   14 split-x GEMM for batch <= 16 on a 16-row tile (16x16x32 MFMA) instead
- *      of the 32-row one [1] */
+ *      of the 32-row one [1]
+ *   15 split-x GEMM on 8-wave workgroups whose two wave groups share each
+ *      unit's k range (one partial tile per workgroup) [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 #ifdef __cplusplus

@@ -76,7 +76,8 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4), dict(bf3_depth=2),
          dict(bf3_depth=3), dict(bf3_depth=3, gemm_occ=1), dict(bf3_cols=1),
          dict(bf3_cols=1, gemm_occ=1), dict(dw_mfma=0), dict(bf3_small=0),
-         dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2)]
+         dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2), dict(bf3_groups=0),
+         dict(bf3_depth=1), dict(bf3_groups=0, bf3_depth=2), dict(bf3_groups=1, gemm_occ=2)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -104,6 +105,38 @@ def test_forward_kernel_variants(oracle, knobs):
     finally:
         for k, v in old.items():
             pywelvet.set_tuning(k, v)
+
+
+@pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26])
+def test_split_x_two_group_workgroups(oracle, dtype):
+    """The split-x GEMM on 8-wave workgroups whose two wave groups take
+    alternate k stages and add their sums through LDS at each tile's end:
+    64-row tiles (batch 33-64, ragged batch included) and the 32-row tiles of
+    the 4-bit kinds, K whose last stage runs past it, shares crossing tile
+    boundaries, both ring depths, and the dX of a forward through the
+    transposed codes (K = rows)."""
+    rng = np.random.default_rng(1500 + dtype)
+    cases = ((300, 2016, 64), (257, 1024, 48), (128, 4096, 33), (1000, 512, 64), (300, 2016, 20))
+    for depth in (0, 1):
+        old = pywelvet.set_tuning("bf3_depth", depth)
+        try:
+            for out, inn, batch in cases:
+                W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+                if dtype == 16:
+                    W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+                x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+                check_forward(oracle, dtype, W, x, act=2, bias=rng.normal(0, 0.1, out))
+            W = rng.normal(0, 0.1, (384, 640)).astype(np.float32)
+            x = rng.normal(0, 1, (40, 640)).astype(np.float32)
+            gy = rng.normal(0, 1, (40, 384)).astype(np.float32)
+            pre = rng.normal(0, 1, (40, 384)).astype(np.float32)
+            with pywelvet.Session(W, batch=40, act=-1, dtype=dtype) as s:
+                dX, dW = s.backward(x, pre, gy)
+            _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, -1)
+            assert_close(dX, rdX, 384, f"dX depth {depth}")
+            assert_bit_equal(dW, rdW, f"dW depth {depth}")
+        finally:
+            pywelvet.set_tuning("bf3_depth", old)
 
 
 @pytest.mark.parametrize("dtype", [16, 26, 14, 15])

@@ -1346,6 +1346,228 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
   }
 }
 
+// Workgroup barrier for LDS hand-offs only: this wave's LDS operations are
+// complete (lgkmcnt 0) and its global loads stay in flight, where
+// __syncthreads' fence would also wait for every outstanding load (on this
+// target one counter covers vector-memory loads and stores).  The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// gemm_bf3_kernel with two wave groups per workgroup sharing the k range of
+// each unit: a unit is (tile, stage pair p), and group g (waves 4g .. 4g + 3,
+// the same per-wave tiles as gemm_bf3_kernel) runs stage 2p + g.  At the
+// last unit of a tile in the share the groups add their accumulators through
+// LDS (the x buffers, idle at that point; group 0's sum + group 1's in fp32)
+// and each writes half of the one partial tile.  One workgroup per CU keeps
+// two waves per SIMD, like two 4-wave workgroups per CU, while a launch
+// writes half the partial tiles.  GemmArgs::nst counts stage pairs here.
+template <int BK, int MT, int D, int NC>
+__global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
+  using K3 = B3<BK>;
+  constexpr int BM = 32 * MT, BN = 128 * NC, NW = K3::kWords, NP = K3::kParts;
+  constexpr int XE = BM * kBK / 256;  // x values per thread per stage (8 or 16)
+  constexpr int XT = kBK / XE;        // threads per x row
+  constexpr int P = MT * NC;          // 32 x 32 accumulator pieces per wave
+  static_assert(P % 2 == 0, "the pieces are shared out between the two groups");
+  __shared__ uint16_t Xs[2][2][3][BM][kBf3Row];  // [buffer][group][part][m][k]
+  static_assert(sizeof(Xs) >= (size_t)P * 16 * 256 * sizeof(float), "the exchange fits the x buffers");
+  __shared__ uint2 t3[16];
+  const int tid = threadIdx.x, grp = tid >> 8, gt = tid & 255, lane = tid & 63, wave = gt >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  if constexpr (BK == BK_NF4) {
+    if (tid < 16) {  // NF4 table values split exactly into three bf16 parts
+      const float t = kNf4Tab[tid];
+      const uint32_t hi = f2u(t) & 0xffff0000u;
+      const float r = t - u2f(hi);
+      const uint32_t mid = f2u(r) & 0xffff0000u;
+      const uint32_t lo = f2u(r - u2f(mid));
+      t3[tid] = make_uint2((hi >> 16) | mid, lo >> 16);
+    }
+  }
+  const int T = a.gx * a.gy * a.nst;
+  const int it = blockIdx.x * a.per_block;
+  const int it_end = min(T, it + a.per_block);
+  const int first_tile = it / a.nst;
+  const int xm = gt / XT, xk = (gt % XT) * XE;
+  uint32_t wr[D][NC][NW];
+  float xf[D][XE];
+  uint32_t xin[D];
+  auto unit_m0 = [&](int u) { return (u / a.nst / a.gx) * BM; };
+  auto unit_n0 = [&](int u) { return (u / a.nst % a.gx) * BN; };
+  auto unit_k0 = [&](int u) { return (2 * (u % a.nst) + grp) * kBK; };
+  auto load_w = [&](int u, uint32_t (&w)[NC][NW]) {
+    const int n0 = unit_n0(u), k0 = unit_k0(u);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int row = min(n0 + wave * 32 * NC + c * 32 + j, a.N - 1);
+      const uint8_t *src = a.body + (int64_t)row * a.row_bytes + (k0 + 32 * h) * K3::kBits / 8;
+#pragma unroll
+      for (int i = 0; i < NW; i += 4) {
+        const uint4 v = *(const uint4 *)(src + 4 * i);
+        w[c][i] = v.x; w[c][i + 1] = v.y; w[c][i + 2] = v.z; w[c][i + 3] = v.w;
+      }
+    }
+  };
+  auto load_x = [&](int u, float (&xf)[XE], uint32_t &in_mask) {
+    const int m0 = unit_m0(u), k0 = unit_k0(u);
+    const bool in = m0 + xm < a.M && k0 + xk < a.K;
+    in_mask = in ? ~0u : 0u;
+    const float *src = a.A + (int64_t)(in ? m0 + xm : 0) * a.K + (in ? k0 + xk : 0);
+#pragma unroll
+    for (int i = 0; i < XE; i += 4) {
+      const float4 v = *(const float4 *)(src + i);
+      xf[i] = v.x;
+      xf[i + 1] = v.y;
+      xf[i + 2] = v.z;
+      xf[i + 3] = v.w;
+    }
+  };
+  auto store_x = [&](int buf, const float (&xf)[XE], uint32_t in_mask) {
+    uint32_t wp[3][XE / 2];
+#pragma unroll
+    for (int i = 0; i < XE; i += 2) {
+      uint32_t part[3][2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = u2f(f2u(xf[i + e]) & in_mask);
+        const uint32_t hi = f2u(v) & 0xffff0000u;
+        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const uint32_t mid = f2u(r) & 0xffff0000u;
+        part[0][e] = hi;
+        part[1][e] = mid;
+        part[2][e] = f2u(r - u2f(mid));
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) wp[p][i / 2] = __builtin_amdgcn_perm(part[p][1], part[p][0], 0x07060302u);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int q = 0; q < XE / 8; ++q)
+        *(uint4 *)&Xs[buf][grp][p][xm][xk + 8 * q] =
+            make_uint4(wp[p][4 * q], wp[p][4 * q + 1], wp[p][4 * q + 2], wp[p][4 * q + 3]);
+  };
+  auto mfma_step = [&](floatx16 (&acc)[MT][NC], int buf, int q, const bf16x8 (&bv)[NC][NP]) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 av =
+            __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[buf][grp][p][mt * 32 + j][32 * h + 8 * q]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int wp = 0; wp < NP; ++wp)
+            if (p + wp <= 2)
+              acc[mt][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[c][wp], acc[mt][c], 0, 0, 0);
+      }
+    }
+  };
+  floatx16 acc[MT][NC];
+  int buf = 0;
+  const int last = max(it, it_end - 1);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load_w(min(it + d, last), wr[d]);
+    load_x(min(it + d, last), xf[d], xin[d]);
+  }
+  store_x(0, xf[0], xin[0]);
+  lds_barrier();
+  float *xch = reinterpret_cast<float *>(&Xs[0][0][0][0][0]);
+  for (int u0 = it; u0 < it_end; u0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int u = u0 + d;
+      if (u >= it_end) break;
+      const int t = u / a.nst, st = u - t * a.nst;
+      const bool tile_end = st == a.nst - 1 || u + 1 == it_end;
+      // with the ring two units deep, group 1 stages the next unit's x
+      // before its MFMAs and group 0 after them, so the two waves of a SIMD
+      // overlap one's x split with the other's MFMAs (both after the tile's
+      // end, where the exchange takes the x buffers first)
+      const bool early = D >= 2 && grp == 1 && !tile_end;
+      if (early) store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
+      if (u == it || st == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mt][c][i] = 0.0f;
+      }
+      if constexpr (NP == 1) {
+        bf16x8 bv[4][NC][1];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            bf16x8 pp[1];
+            bf3_weights<BK>(wr[d][c], q, t3, pp);
+            bv[q][c][0] = pp[0];
+          }
+        load_w(min(u + D, last), wr[d]);
+        load_x(min(u + D, last), xf[d], xin[d]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mfma_step(acc, buf, q, bv[q]);
+      } else {
+        load_x(min(u + D, last), xf[d], xin[d]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bf16x8 bv[NC][NP];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) bf3_weights<BK>(wr[d][c], q, t3, bv[c]);
+          mfma_step(acc, buf, q, bv);
+        }
+        load_w(min(u + D, last), wr[d]);
+      }
+      if (tile_end) {
+        // piece pc = mt * NC + c: group 0 keeps pieces 0 .. P/2 - 1, group 1
+        // the rest; each group leaves the other's pieces in region grp of the
+        // exchange, lane-major (same wave index and lane = same outputs)
+        lds_barrier();  // every wave is done reading x from LDS
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int pc = mt * NC + c;
+            if ((pc < P / 2) != (grp == 0)) {
+              float *dst = xch + (size_t)(grp * (P / 2) + pc % (P / 2)) * 16 * 256 + gt;
+#pragma unroll
+              for (int r = 0; r < 16; ++r) dst[r * 256] = acc[mt][c][r];
+            }
+          }
+        lds_barrier();
+        float *dst = a.ws + ((int64_t)blockIdx.x * a.maxspan + (t - first_tile)) * (BM * BN);
+        const int mrows = a.M - unit_m0(u);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int pc = mt * NC + c;
+            if ((pc < P / 2) == (grp == 0)) {
+              const float *src = xch + (size_t)((1 - grp) * (P / 2) + pc % (P / 2)) * 16 * 256 + gt;
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const float v = acc[mt][c][r] + src[r * 256];
+                const int m = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (mt * 32 + 8 * (r >> 2) < mrows) dst[m * BN + wave * 32 * NC + c * 32 + j] = v;
+              }
+            }
+          }
+        lds_barrier();  // the exchange is read before x goes back into the buffers
+      }
+      if (!early) store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
+      lds_barrier();
+      buf ^= 1;
+    }
+  }
+}
+
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // The split-x GEMM for batch <= 16: one 16-row tile on
@@ -1977,7 +2199,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 1, 0, 2, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -2055,17 +2277,20 @@ struct SkPlan {
   int gx, gy, nst, per_block, blocks, maxspan, bm, bn;
   size_t ws_bytes;
   bool bf3 = false;  // split-x GEMM plan (bn = 128 or 256)
+  int kg = 1;        // k stages per unit: 2 = the two-group split-x GEMM
 };
 
 // Stream-K split of an M x N x K product over bm x bn tiles into equal
-// shares, `occ` workgroups per CU.
-SkPlan plan_sk(int M, int K, int N, int bm = kBM, int bn = kBN, int occ = 2) {
+// shares, `occ` workgroups per CU; units of `kg` consecutive k stages (the
+// caller makes the stage count a multiple of kg).
+SkPlan plan_sk(int M, int K, int N, int bm = kBM, int bn = kBN, int occ = 2, int kg = 1) {
   SkPlan p;
   p.bm = bm;
   p.bn = bn;
+  p.kg = kg;
   p.gx = (N + bn - 1) / bn;
   p.gy = (M + bm - 1) / bm;
-  p.nst = (K + kBK - 1) / kBK;
+  p.nst = (K + kBK - 1) / kBK / kg;
   const int64_t T = (int64_t)p.gx * p.gy * p.nst;
   const int64_t G = (int64_t)occ * num_cus();
   p.per_block = (int)((T + G - 1) / G);
@@ -2089,7 +2314,13 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
     const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
     const int bm = (M <= 16 && g_tune[kTuneBf3Small] != 0) ? 16 : M <= 32 ? 32 : 64;
-    SkPlan p = plan_sk(M, K, N, bm, bn, occ);
+    const int stages = (K + kBK - 1) / kBK;
+    // two-group workgroups: every 64-row tile; 32-row tiles only for the
+    // 4-bit kinds (FP8 / Int8 measured slower there)
+    const bool groups = g_tune[kTuneBf3Groups] != 0 && bn == 256 && stages % 2 == 0 &&
+                        (bm == 64 || (bm == 32 && (bk == BK_NF4 || bk == BK_FP4)));
+    SkPlan p = groups ? plan_sk(M, K, N, bm, bn, g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 1, 2)
+                      : plan_sk(M, K, N, bm, bn, occ);
     p.bf3 = true;
     return p;
   }
@@ -2185,6 +2416,26 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
     if (p.bn == 128) gemm_bf3_kernel<BK, 2, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
     else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
     else gemm_bf3_kernel<BK, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
+  }
+  if (p.kg == 2) {  // ring depth 2 unless the knob asks for 1
+#define WH_GK(BK)                                                                             \
+  if (p.bm == 32) {                                                                           \
+    if (dep == 1) gemm_bf3k_kernel<BK, 1, 1, 2><<<p.blocks, 512, 0, s>>>(a);                  \
+    else gemm_bf3k_kernel<BK, 1, 2, 2><<<p.blocks, 512, 0, s>>>(a);                           \
+  } else {                                                                                    \
+    if (dep == 1) gemm_bf3k_kernel<BK, 2, 1, 2><<<p.blocks, 512, 0, s>>>(a);                  \
+    else gemm_bf3k_kernel<BK, 2, 2, 2><<<p.blocks, 512, 0, s>>>(a);                           \
+  }
+    switch (bk) {
+    case BK_E4: WH_GK(BK_E4) break;
+    case BK_I8: WH_GK(BK_I8) break;
+    case BK_FP4: WH_GK(BK_FP4) break;
+    case BK_NF4: WH_GK(BK_NF4) break;
+    case BK_E5: WH_GK(BK_E5) break;
+    default: return hipErrorInvalidValue;
+    }
+#undef WH_GK
+    return hipGetLastError();
   }
   switch (bk) {
   case BK_E4: WH_GB(BK_E4, 1) break;

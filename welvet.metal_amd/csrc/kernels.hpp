@@ -103,16 +103,20 @@ void set_forward_path(int path);
 // block per row group; -1 = auto: 16 for the FP8 and FP4 converter formats,
 // else 0).
 // 10 split-x bf16 MFMA GEMM for FP8 E4M3 / E5M2, Int8, FP4 and NF4 (1 on), 11 its weight
-// prefetch depth in k stages (1, 2, or 3 for batch <= 32), 12 its block
+// prefetch depth in k stages (0 auto: 1, and 2 on two-group workgroups; 1, 2, or 3 for
+// batch <= 32), 12 its block
 // width (0: 256 output columns, 1: 128).  13 dW kernel, all bit-identical to the
 // sequential FMA: 2 fp32 MFMA with operands staged in LDS (shapes of whole
 // 128-tiles; others take 1), 1 fp32 MFMA with direct loads, 0 VALU.  14 the
 // split-x GEMM's 16-row tile on the 16x16x32 MFMA for batch <= 16 (1 on).
+// 15 the split-x GEMM's two-group workgroups (8 waves sharing each unit's
+// k range, one partial tile per workgroup) for 32- and 64-row tiles of 256
+// columns when the k stages pair up (1 on).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kNumTune = 15
+  kTuneBf3Groups = 15, kNumTune = 16
 };
 int set_tuning(int key, int value);
 
