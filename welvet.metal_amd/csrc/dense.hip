@@ -1473,8 +1473,8 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
   const int last = max(it, it_end - 1);
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    load_w(min(it + d, last), wr[d]);
     load_x(min(it + d, last), xf[d], xin[d]);
+    load_w(min(it + d, last), wr[d]);
   }
   store_x(0, xf[0], xin[0]);
   lds_barrier();
@@ -1483,7 +1483,9 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int u = u0 + d;
-      if (u >= it_end) break;
+      // leaving the whole loop (not just this unrolled step) keeps the
+      // compiler's wait counts for the ring exact: no path runs a step twice
+      if (u >= it_end) goto done;
       const int t = u / a.nst, st = u - t * a.nst;
       const bool tile_end = st == a.nst - 1 || u + 1 == it_end;
       // with the ring two units deep, group 1 stages the next unit's x
@@ -1510,8 +1512,8 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
             bf3_weights<BK>(wr[d][c], q, t3, pp);
             bv[q][c][0] = pp[0];
           }
+        load_x(min(u + D, last), xf[d], xin[d]);  // first: the early x store waits for it alone
         load_w(min(u + D, last), wr[d]);
-        load_x(min(u + D, last), xf[d], xin[d]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) mfma_step(acc, buf, q, bv[q]);
       } else {
@@ -1562,10 +1564,16 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
         lds_barrier();  // the exchange is read before x goes back into the buffers
       }
       if (!early) store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
+      // every wave has now stored the next unit's x, early or late; a use
+      // on both paths lets the compiler see that, so it does not wait for
+      // those loads again where the slot's registers are reused
+#pragma unroll
+      for (int i = 0; i < XE; ++i) asm volatile("" ::"v"(xf[(d + 1) % D][i]));
       lds_barrier();
       buf ^= 1;
     }
   }
+done:;
 }
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
