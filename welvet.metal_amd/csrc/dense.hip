@@ -137,6 +137,18 @@ __device__ inline void load_words(const uint8_t *__restrict__ p, uint32_t (&w)[W
   }
 }
 
+// Workgroup barrier for LDS hand-offs only: this wave's LDS operations are
+// complete (lgkmcnt 0) and its global loads stay in flight, where
+// __syncthreads' fence would also wait for every outstanding load (on this
+// target one counter covers vector-memory loads and stores).  The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // load_words with the non-temporal hint (streamed weights, read once).
 template <int W>
 __device__ inline void load_words_nt(const uint8_t *__restrict__ p, uint32_t (&w)[W]) {
@@ -1346,18 +1358,6 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
   }
 }
 
-// Workgroup barrier for LDS hand-offs only: this wave's LDS operations are
-// complete (lgkmcnt 0) and its global loads stay in flight, where
-// __syncthreads' fence would also wait for every outstanding load (on this
-// target one counter covers vector-memory loads and stores).  The empty asm
-// statements keep the compiler from moving memory accesses across it.
-__device__ inline void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // gemm_bf3_kernel with two wave groups per workgroup sharing the k range of
 // each unit: a unit is (tile, stage pair p), and group g (waves 4g .. 4g + 3,
 // the same per-wave tiles as gemm_bf3_kernel) runs stage 2p + g.  At the
@@ -2509,9 +2509,12 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         // group)
         const int ngroups = (a.N + R - 1) / R;
         int wpc = g_tune[kTuneGemvWaves];
-        if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
         int blocks = ngroups;
-        if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
+        if (wpc < -1) blocks = (ngroups - wpc - 1) / -wpc;  // -k: k row groups per block
+        else {
+          if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
+          if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
+        }
 #define WH_PF(F)                                                                         \
   if constexpr (F == FE4 || F == FE5 || F == FF4) {                                      \
     if (blocks < ngroups) {                                                              \
