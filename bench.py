@@ -16,7 +16,9 @@ on the stream the kernels are launched on (an explicit torch stream handed to
 the library), K back-to-back steps between them after W warm-up steps.
 
 roofline.traffic comes from the committed rocprofv3 --pmc passes
-(profiles/hbm_traffic.json); it is not measured live.
+(profiles/hbm_traffic.json); it is not measured live.  roofline.read_floor
+(batch-1 primary) is measured live: the library's streaming-read probe over
+the same bytes, rotated and timed like the steps.
 
 cpu_baseline: the oracle's scalar port of the reference host path (per-element
 decode switch + f64 dot, oracle/oracle.c or_dense_forward_native) on full
@@ -107,6 +109,34 @@ def run_case(torch, pywelvet, dtype: int, batch: int, steps: int, warmup: int, s
     for s in sessions:
         s.close()
     return r
+
+
+def read_floor(torch, pywelvet, nbytes: int, steps: int, warmup: int):
+    """The single-launch read floor for a case's packed bytes: the library's
+    streaming-read probe (welvet_hip_probe_read) over the same number of
+    bytes, rotating through copies larger than the MALL and timed like the
+    case's steps, so value / floor says how much of what one launch can read
+    the kernel reaches."""
+    dev = torch.device("cuda:0")
+    n = (nbytes + 15) // 16 * 16
+    copies = max(2, -(-MALL_BYTES // n))
+    bufs = [torch.full((n,), i, dtype=torch.uint8, device=dev) for i in range(copies)]
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)  # default priority
+    sh = stream.cuda_stream
+    for i in range(warmup):
+        pywelvet.probe_read(bufs[i % copies].data_ptr(), n, sink.data_ptr(), sh)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        pywelvet.probe_read(bufs[i % copies].data_ptr(), n, sink.data_ptr(), sh)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    return {"kernel": "read_probe_kernel (16-byte non-temporal loads, four in flight per thread)",
+            "bytes": n, "copies": copies, "us": ms * 1e3, "gbs": n / (ms * 1e-3) / 1e9}
 
 
 def cpu_model() -> str:
@@ -499,6 +529,11 @@ def main():
         ach = prim["hbm_gbs"]
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK, "unit": "GB/s",
                 "frac": ach / HBM_PEAK, "traffic": measured_traffic(prim_name(results, prim))}
+        fl = read_floor(torch, pywelvet, prim["packed_bytes"], a.steps, min(a.warmup, 500))
+        fl["frac_of_floor"] = ach / fl["gbs"]
+        roof["read_floor"] = fl
+        print(f"# read floor ({fl['bytes']} B): {fl['gbs']:.1f} GB/s  {fl['us']:.2f} us/launch",
+              file=sys.stderr, flush=True)
     else:
         roof = {"bound": "mfma", "achieved": prim["executed_tflops"], "peak": prim["peak_tflops"],
                 "unit": "TFLOP/s", "frac": prim["roofline_frac"],

@@ -355,6 +355,16 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      unit's k range (one partial tile per workgroup) [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
+/* No counterpart in the reference: a measurement aid.  Streams `bytes`
+ * (a non-zero multiple of 16) of device memory at d_bytes once, in one
+ * launch on `stream`, with the loads the batch-1 GEMVs use (16 bytes per
+ * lane, non-temporal, four in flight per thread); the single-launch floor
+ * for a kernel that reads the same bytes once.  d_sink: 4 KB of device
+ * memory the probe may write (practically never does).  Code 1 on null or
+ * misaligned arguments. */
+WELVET_API welvet_status welvet_hip_probe_read(const void *d_bytes, uint64_t bytes, void *d_sink,
+                                               void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -463,3 +463,27 @@ def test_normalbp_error_codes():
     assert r["status"].code == 1
     r = pywelvet.normalbp(W, x, np.zeros((1, 2), np.float32), 1, 0.0, dtype=9)
     assert r["loss"] >= 0
+
+
+def test_read_probe():
+    """welvet_hip_probe_read (the bench's single-launch read floor) streams a
+    buffer without writing the sink in practice, and refuses misaligned or
+    ragged arguments with code 1."""
+    from devmem import DeviceArray, Stream
+
+    buf = DeviceArray((1 << 20,), fill=1.0)   # 4 MiB
+    sink = DeviceArray((1024,), fill=0.0)
+    st = Stream()
+    try:
+        pywelvet.probe_read(buf.ptr, buf.nbytes, sink.ptr, st.h)
+        pywelvet.probe_read(buf.ptr, 48, sink.ptr, st.h)   # less than one block
+        st.sync()
+        assert np.all(sink.download() == 0.0)
+        for args in ((buf.ptr + 4, 1024), (buf.ptr, 1000), (buf.ptr, 0)):
+            s = pywelvet.lib().welvet_hip_probe_read(pywelvet.C.c_void_p(args[0]), pywelvet.C.c_uint64(args[1]),
+                                                     pywelvet.C.c_void_p(sink.ptr), pywelvet.C.c_void_p(st.h))
+            assert s.code == 1, args
+    finally:
+        st.close()
+        buf.free()
+        sink.free()

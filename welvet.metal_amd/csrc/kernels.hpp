@@ -85,6 +85,10 @@ hipError_t launch_mse(const float *pred, const float *target, int64_t n, double 
                       void *ws, size_t ws_bytes, hipStream_t s);
 size_t mse_workspace_bytes(int64_t n);
 
+// Reads `bytes` (a multiple of 16) at p once, 16 bytes per load; sink: 1024
+// words the kernel practically never writes.
+hipError_t launch_read_probe(const void *p, int64_t bytes, uint32_t *sink, hipStream_t s);
+
 // Kernel-selection knobs, exposed for sweeps: forward path for a batch
 // (0 = auto, 1 = GEMV, 2 = MFMA GEMM, 3 = generic element-wise).
 void set_forward_path(int path);

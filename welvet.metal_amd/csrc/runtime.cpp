@@ -809,4 +809,12 @@ void welvet_hip_set_forward_path(int32_t path) { set_forward_path(path); }
 
 int32_t welvet_hip_set_tuning(int32_t key, int32_t value) { return set_tuning(key, value); }
 
+welvet_status welvet_hip_probe_read(const void *d_bytes, uint64_t bytes, void *d_sink, void *stream) {
+  if (!d_bytes || !d_sink) return make_status(kInvalid, "null probe args");
+  if ((((uintptr_t)d_bytes | (uintptr_t)d_sink) & 15) || bytes == 0 || bytes % 16)
+    return make_status(kInvalid, "probe: 16-byte aligned pointers and a non-zero multiple of 16 bytes");
+  WH_HIP(launch_read_probe(d_bytes, (int64_t)bytes, (uint32_t *)d_sink, (hipStream_t)stream));
+  return ok();
+}
+
 }  // extern "C"

@@ -159,6 +159,8 @@ def lib() -> C.CDLL:
         L.welvet_hip_set_forward_path.restype = None
         L.welvet_hip_set_tuning.argtypes = [_i32, _i32]
         L.welvet_hip_set_tuning.restype = _i32
+        L.welvet_hip_probe_read.argtypes = [_vp, C.c_uint64, _vp, _vp]
+        L.welvet_hip_probe_read.restype = Status
         coord = [_vp] + [_i32] * 4
         L.welvet_hip_grid_new.argtypes = [_i32] * 5 + [C.POINTER(_vp)]
         L.welvet_hip_grid_new.restype = Status
@@ -223,6 +225,13 @@ TUNE = {"gemv1": 0, "rows_per_block": 1, "acc64": 2, "cr": 3, "reg_gemm": 4, "ge
 
 def set_tuning(key: str, value: int) -> int:
     return lib().welvet_hip_set_tuning(TUNE[key], int(value))
+
+
+def probe_read(d_bytes: int, nbytes: int, d_sink: int, stream: int = 0) -> None:
+    """welvet_hip_probe_read: stream nbytes of device memory once (a floor
+    measurement); raises on a non-zero status."""
+    check(lib().welvet_hip_probe_read(C.c_void_p(d_bytes), C.c_uint64(nbytes), C.c_void_p(d_sink),
+                                      C.c_void_p(stream)))
 
 
 def forward(W, x, act=-1, dtype=1, bias=None, status=False):
