@@ -1774,13 +1774,29 @@ __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double
       }
     }
   }
+  // the epilogue of bias_act_store (or fl32 for dX) on the four sums, stored
+  // as one 16-byte write per output array where the row allows it
+  float pv[4], qv[4];
+  const int nv = min(4, a.N - n);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (n + i >= a.N) break;
-    const int64_t idx = (int64_t)m * a.N + n + i;
     if (a.post != 1.0f) sum[i] *= (double)a.post;
-    if constexpr (FWD) bias_act_store(sum[i], n + i, bias, bias_len, act, out, post, idx);
-    else out[idx] = (float)sum[i];
+    float p = (float)sum[i];
+    if constexpr (FWD) {
+      if (bias != nullptr && n + i < bias_len) p = (float)((double)p + bias[n + i]);
+      qv[i] = i < nv ? act_value(p, act) : 0.0f;
+    }
+    pv[i] = p;
+  }
+  const int64_t idx = (int64_t)m * a.N + n;
+  if (nv == 4 && (a.N & 3) == 0) {
+    *(float4 *)(out + idx) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+    if constexpr (FWD) *(float4 *)(post + idx) = make_float4(qv[0], qv[1], qv[2], qv[3]);
+  } else {
+    for (int i = 0; i < nv; ++i) {
+      out[idx + i] = pv[i];
+      if constexpr (FWD) post[idx + i] = qv[i];
+    }
   }
 }
 
