@@ -1471,13 +1471,18 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
   floatx16 acc[MT][NC];
   int buf = 0;
   const int last = max(it, it_end - 1);
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    load_x(min(it + d, last), xf[d], xin[d]);
-    load_w(min(it + d, last), wr[d]);
-  }
+  // the first unit's loads go out alone: every workgroup asks at once, and
+  // the later units' requests would queue in front of them
+  load_x(it, xf[0], xin[0]);
+  load_w(it, wr[0]);
   store_x(0, xf[0], xin[0]);
   lds_barrier();
+#pragma unroll
+  for (int d = 1; d < D; ++d) {
+    load_x(min(it + d, last), xf[d], xin[d]);
+    __builtin_amdgcn_sched_barrier(0);  // x before w, as in the loop (wait counts)
+    load_w(min(it + d, last), wr[d]);
+  }
   float *xch = reinterpret_cast<float *>(&Xs[0][0][0][0][0]);
   for (int u0 = it; u0 < it_end; u0 += D) {
 #pragma unroll
@@ -1491,8 +1496,9 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
       // with the ring two units deep, group 1 stages the next unit's x
       // before its MFMAs and group 0 after them, so the two waves of a SIMD
       // overlap one's x split with the other's MFMAs (both after the tile's
-      // end, where the exchange takes the x buffers first)
-      const bool early = D >= 2 && grp == 1 && !tile_end;
+      // end, where the exchange takes the x buffers first, and on the first
+      // unit, whose successor's x was only just requested)
+      const bool early = D >= 2 && grp == 1 && !tile_end && u != it;
       if (early) store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
       if (u == it || st == 0) {
 #pragma unroll
