@@ -78,7 +78,7 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(bf3_cols=1, gemm_occ=1), dict(dw_mfma=0), dict(bf3_small=0),
          dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2), dict(bf3_groups=0),
          dict(bf3_depth=1), dict(bf3_groups=0, bf3_depth=2), dict(bf3_groups=1, gemm_occ=2),
-         dict(gemv_waves=-2), dict(gemv_waves=-3)]
+         dict(gemv_waves=-2), dict(gemv_waves=-3), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
@@ -171,7 +171,7 @@ def test_split_x_small_batch_tile(oracle, dtype, batch):
     Wd = oracle_weights(oracle, dtype, W)
     _, rdX, rdW = oracle.backward(Wd, x, pre, gy, -1)
     for knobs in (dict(bf3_small=1), dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2),
-                  dict(bf3_small=0)):
+                  dict(bf3_small=0), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2)):
         old = {k: pywelvet.set_tuning(k, v) for k, v in knobs.items()}
         try:
             check_forward(oracle, dtype, W, x)

@@ -1743,6 +1743,150 @@ __global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
   }
 }
 
+// The split-x GEMM for batch <= 16 with no k split across workgroups: a
+// workgroup owns 32 output columns (two waves of 16) over the whole of K,
+// and its four wave groups take every fourth 64-deep k stage (group g:
+// stages g, g + 4, ...), each staging its own stage's x parts in LDS.  At
+// the end the groups' fp32 sums meet in LDS, are added in group order in f64
+// and the epilogue (post scale, then bias and activation for the forward,
+// fl32 for dX) stores the outputs directly: no partial tiles and no
+// reduction launch.  Operand layout, x split and weight decode are
+// gemm_bf3s_kernel's (16x16x32 MFMA; a lane holds 16 consecutive weights of
+// one column per stage).  Rounds past a group's last stage re-read a valid
+// stage against x masked to zero.
+template <int BK, int D, bool FWD>
+__global__ void __launch_bounds__(512) gemm_bf3r_kernel(GemmArgs a, const double *bias, int bias_len,
+                                                        int act, float *out, float *post) {
+  using K3 = B3<BK>;
+  constexpr int KG = 4, CW = 2, BM = 16, NW = K3::kWords / 2, NP = K3::kParts;
+  constexpr int XE = BM * kBK / 128;  // 8 x values per thread per stage (128 threads per group)
+  constexpr int XT = kBK / XE;        // 8 threads per x row
+  static_assert(XE == 8 && (NW == 2 || NW == 4), "16-row split-x layout");
+  __shared__ uint16_t Xs[2][KG][3][BM][kBf3Row];
+  __shared__ float ex[KG - 1][CW][4][64];
+  __shared__ uint2 t3[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int grp = wv / CW, cw = wv % CW, gt = tid & 127;
+  const int j = lane & 15, g = lane >> 4;
+  if constexpr (BK == BK_NF4) {
+    if (tid < 16) {  // NF4 table values split exactly into three bf16 parts
+      const float t = kNf4Tab[tid];
+      const uint32_t hi = f2u(t) & 0xffff0000u;
+      const float r = t - u2f(hi);
+      const uint32_t mid = f2u(r) & 0xffff0000u;
+      const uint32_t lo = f2u(r - u2f(mid));
+      t3[tid] = make_uint2((hi >> 16) | mid, lo >> 16);
+    }
+  }
+  const int n0 = blockIdx.x * (16 * CW), m0 = blockIdx.y * BM;
+  const int rounds = (a.nst + KG - 1) / KG;
+  const int xm = gt / XT, xk = (gt % XT) * XE;  // xm < 16, xk < 64
+  const int col = n0 + cw * 16 + j;
+  const int64_t wrow = (int64_t)min(col, a.N - 1) * a.row_bytes;
+  uint32_t wr[D][NW];
+  float xf[D][XE];
+  uint32_t xin[D];
+  auto load_w = [&](int r, uint32_t (&w)[NW]) {
+    const int k0 = min(grp + KG * r, a.nst - 1) * kBK;
+    const uint8_t *src = a.body + wrow + (k0 + 16 * g) * K3::kBits / 8;
+    if constexpr (NW == 4) {
+      const uint4 v = *(const uint4 *)src;
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+      const uint2 v = *(const uint2 *)src;
+      w[0] = v.x; w[1] = v.y;
+    }
+  };
+  auto load_x = [&](int r, float (&xv)[XE], uint32_t &in_mask) {
+    const int k0 = (grp + KG * r) * kBK;
+    const bool in = m0 + xm < a.M && k0 + xk < a.K;
+    in_mask = in ? ~0u : 0u;
+    const float *src = a.A + (int64_t)(in ? m0 + xm : 0) * a.K + (in ? k0 + xk : 0);
+    const float4 v0 = *(const float4 *)src, v1 = *(const float4 *)(src + 4);
+    xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+    xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+  };
+  auto store_x = [&](int buf, const float (&xv)[XE], uint32_t in_mask) {
+    uint32_t wp[3][XE / 2];
+#pragma unroll
+    for (int i = 0; i < XE; i += 2) {
+      uint32_t part[3][2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = u2f(f2u(xv[i + e]) & in_mask);
+        const uint32_t hi = f2u(v) & 0xffff0000u;
+        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const uint32_t mid = f2u(r) & 0xffff0000u;
+        part[0][e] = hi;
+        part[1][e] = mid;
+        part[2][e] = f2u(r - u2f(mid));
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) wp[p][i / 2] = __builtin_amdgcn_perm(part[p][1], part[p][0], 0x07060302u);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      *(uint4 *)&Xs[buf][grp][p][xm][xk] = make_uint4(wp[p][0], wp[p][1], wp[p][2], wp[p][3]);
+  };
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto mfma_step = [&](int buf, int q, const bf16x8 (&bv)[NP]) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const bf16x8 av = __builtin_bit_cast(bf16x8, *(const shortx8 *)&Xs[buf][grp][p][j][16 * g + 8 * q]);
+#pragma unroll
+      for (int wp = 0; wp < NP; ++wp)
+        if (p + wp <= 2) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[wp], acc, 0, 0, 0);
+    }
+  };
+  int buf = 0;
+  const int last = rounds - 1;
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load_x(min(d, last), xf[d], xin[d]);
+    load_w(min(d, last), wr[d]);
+  }
+  store_x(0, xf[0], xin[0]);
+  lds_barrier();
+  for (int r0 = 0; r0 < rounds; r0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int r = r0 + d;
+      if (r >= rounds) goto done;
+      bf16x8 bv[2][NP];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) bf3_weights<BK>(wr[d], q, t3, bv[q]);
+      load_x(min(r + D, last), xf[d], xin[d]);
+      load_w(min(r + D, last), wr[d]);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) mfma_step(buf, q, bv[q]);
+      store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
+      lds_barrier();
+      buf ^= 1;
+    }
+  }
+done:
+  // D lane (j, g) holds column j, rows 4 g .. 4 g + 3 of the group's sum
+  if (grp > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ex[grp - 1][cw][i][lane] = acc[i];
+  }
+  lds_barrier();
+  if (grp == 0 && col < a.N) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + 4 * g + i;
+      if (m >= a.M) break;
+      double sum = (double)acc[i];
+#pragma unroll
+      for (int q = 0; q < KG - 1; ++q) sum += (double)ex[q][cw][i][lane];
+      if (a.post != 1.0f) sum *= (double)a.post;
+      const int64_t idx = (int64_t)m * a.N + col;
+      if constexpr (FWD) bias_act_store(sum, col, bias, bias_len, act, out, post, idx);
+      else out[idx] = (float)sum;
+    }
+  }
+}
+
 // Sum of a tile's stream-K partials in workgroup order (f64).  Grid: x =
 // tile, y = 1024-element slice of the tile; each thread adds four adjacent
 // outputs with float4 loads.  The forward applies bias + activation, dX
@@ -2229,7 +2373,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -2308,6 +2452,7 @@ struct SkPlan {
   size_t ws_bytes;
   bool bf3 = false;  // split-x GEMM plan (bn = 128 or 256)
   int kg = 1;        // k stages per unit: 2 = the two-group split-x GEMM
+  bool rows = false;  // gemm_bf3r_kernel: whole K per workgroup, no partials
 };
 
 // Stream-K split of an M x N x K product over bm x bn tiles into equal
@@ -2345,6 +2490,24 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
     const int bm = (M <= 16 && g_tune[kTuneBf3Small] != 0) ? 16 : M <= 32 ? 32 : 64;
     const int stages = (K + kBK - 1) / kBK;
+    // no k split for K <= 2048 (measured at batch 5-16: 1024^2 6.6 against
+    // 10.3 us, 2048 -> 4096 9.4 against 14.3; at K = 4096 about even, at
+    // K = 11008 1.6x slower: too few workgroups for the serial K walk)
+    const int rk = g_tune[kTuneBf3Rows];
+    if (bm == 16 && K % 8 == 0 && (rk == 2 || (rk == 1 && K <= 2048))) {
+      SkPlan p;
+      p.bf3 = p.rows = true;
+      p.bm = 16;
+      p.bn = 32;
+      p.gx = (N + 31) / 32;
+      p.gy = (M + 15) / 16;
+      p.nst = stages;
+      p.per_block = stages;
+      p.blocks = p.gx * p.gy;
+      p.maxspan = 1;
+      p.ws_bytes = 0;
+      return p;
+    }
     // two-group workgroups: every 64-row tile; 32-row tiles only for the
     // 4-bit kinds (FP8 / Int8 measured slower there)
     const bool groups = g_tune[kTuneBf3Groups] != 0 && bn == 256 && stages % 2 == 0 &&
@@ -2366,7 +2529,13 @@ constexpr int kDxSegRows = 32;
 int fwd_route(const DevStore &w, int batch) {
   if (!chunk_aligned(w, w.cols)) return 3;
   if (g_forward_path) return g_forward_path;
-  return batch <= 4 ? 1 : 2;
+  if (batch <= 2) return 1;
+  if (batch > 4) return 2;
+  // batch 3-4: the GEMV re-reads x for every chunk, so its time grows with
+  // the batch, while the split-x GEMM's does not; measured crossover between
+  // 16.8 M weights (4096^2: GEMV 12.5 against 15.3 us at batch 4) and 45 M
+  // (4096 x 11008: 22.1 against 19.4 us FP8, 32.3 against 22.0 NF4)
+  return (bf3_kind(w) < 0 || (int64_t)w.rows * w.cols <= (int64_t)32 << 20) ? 1 : 2;
 }
 
 template <int F, int B>
@@ -2429,6 +2598,28 @@ size_t forward_workspace_bytes(const DevStore &w, int batch) {
   return plan_fwd_gemm(kernel_fmt(w.dtype), bf3_kind(w), batch, w.cols, w.rows).ws_bytes;
 }
 
+// gemm_bf3r_kernel for plan p (p.rows): the forward (bias, activation, pre
+// and post) or dX (out only, FWD false).
+template <bool FWD>
+hipError_t launch_bf3r(const SkPlan &p, int bk, const GemmArgs &a, const double *bias, int bias_len,
+                       int act, float *out, float *post, hipStream_t s) {
+  const dim3 grid(p.gx, p.gy);
+  const bool d2 = g_tune[kTuneBf3Depth] == 2;
+#define WH_GR3(BK)                                                                                  \
+  if (d2) gemm_bf3r_kernel<BK, 2, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);      \
+  else gemm_bf3r_kernel<BK, 4, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);
+  switch (bk) {
+  case BK_E4: WH_GR3(BK_E4) break;
+  case BK_I8: WH_GR3(BK_I8) break;
+  case BK_FP4: WH_GR3(BK_FP4) break;
+  case BK_NF4: WH_GR3(BK_NF4) break;
+  case BK_E5: WH_GR3(BK_E5) break;
+  default: return hipErrorInvalidValue;
+  }
+#undef WH_GR3
+  return hipGetLastError();
+}
+
 // The split-x GEMM of plan p for weight kind bk (a.body, a.post set).
 hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
   const int dep = g_tune[kTuneBf3Depth];
@@ -2447,6 +2638,7 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
     else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
     else gemm_bf3_kernel<BK, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
   }
+  if (p.rows) return hipErrorInvalidValue;  // launched with its epilogue by the caller
   if (p.kg == 2) {  // ring depth 2 unless the knob asks for 1
 #define WH_GK(BK)                                                                             \
   if (p.bm == 32) {                                                                           \
@@ -2598,6 +2790,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   if (p.bf3) {
     a.post = (bk == BK_I8 || bk == BK_NF4) ? w.scale : 1.0f;
     if (bk == BK_E4 || bk == BK_E5) a.body = w.kbody;
+    if (p.rows) return launch_bf3r<true>(p, bk, a, bias, bias_len, act, pre, post, s);
     const hipError_t e = launch_bf3(p, bk, a, s);
     if (e != hipSuccess) return e;
   } else if (p.bn == kRegBN) {
@@ -2703,9 +2896,13 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     GemmArgs a{w.tbody, w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, (int64_t)w.rows,
                p.gx, p.gy, p.nst, p.per_block, p.maxspan, (float *)ws, p.bm, p.bn};
     a.post = bk == BK_I8 ? w.scale : 1.0f;
-    e = launch_bf3(p, bk, a, s);
-    if (e != hipSuccess) return e;
-    sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
+    if (p.rows) {
+      e = launch_bf3r<false>(p, bk, a, nullptr, 0, -1, dX, nullptr, s);
+    } else {
+      e = launch_bf3(p, bk, a, s);
+      if (e != hipSuccess) return e;
+      sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
+    }
   } else {
     const SkPlan p = plan_sk(batch, w.rows, w.cols);
     GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),

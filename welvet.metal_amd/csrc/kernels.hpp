@@ -115,12 +115,15 @@ void set_forward_path(int path);
 // split-x GEMM's 16-row tile on the 16x16x32 MFMA for batch <= 16 (1 on).
 // 15 the split-x GEMM's two-group workgroups (8 waves sharing each unit's
 // k range, one partial tile per workgroup) for 32- and 64-row tiles of 256
-// columns when the k stages pair up (1 on).
+// columns when the k stages pair up (1 on).  16 for batch <= 16: the split-x
+// GEMM without a k split across workgroups (32 columns per workgroup over all
+// of K, four wave groups on alternate stages, epilogue in the kernel, no
+// reduction launch): 0 off, 1 for K <= 2048, 2 always.
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kTuneBf3Groups = 15, kNumTune = 16
+  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kNumTune = 17
 };
 int set_tuning(int key, int value);
 
