@@ -298,36 +298,50 @@ __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ bod
 // code load, four float4 gradient loads and 16-byte stores (of the
 // decode-ready copy too, for FP8); the first block's threads take the
 // n mod 16 tail.  The per-element arithmetic is sgd_kernel's.
-template <int DT>
+template <int DT, int G>
 __global__ void __launch_bounds__(kThreads) sgd8_kernel(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody,
                                                         int64_t n, const float *__restrict__ g, double lr,
                                                         float scale, float minv, int *stop, const int *bad,
                                                         int bad_value) {
   static_assert(dtype_bits(DT) == 8 && fix_bytes<DT>() == 1, "one-byte codes");
+  static_assert(G == 4 || G == 16, "elements per thread");
+  constexpr int NWD = G / 4;  // code words per thread
   if (sgd_stopped(stop, bad, bad_value)) return;
-  const int64_t groups = n / 16;
+  const int64_t groups = n / G;
   for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < groups; q += (int64_t)gridDim.x * kThreads) {
-    const int64_t i0 = q * 16;
-    const uint4 cv = *(const uint4 *)(body + i0);
-    const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
-    float gv[16];
+    const int64_t i0 = q * G;
+    uint32_t cw[NWD];
+    if constexpr (G == 16) {
+      const uint4 cv = *(const uint4 *)(body + i0);
+      cw[0] = cv.x; cw[1] = cv.y; cw[2] = cv.z; cw[3] = cv.w;
+    } else {
+      cw[0] = *(const uint32_t *)(body + i0);
+    }
+    float gv[G];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < NWD; ++v) {
       const float4 t = *(const float4 *)(g + i0 + 4 * v);
       gv[4 * v] = t.x; gv[4 * v + 1] = t.y; gv[4 * v + 2] = t.z; gv[4 * v + 3] = t.w;
     }
-    uint32_t ow[4] = {0, 0, 0, 0}, kw[4] = {0, 0, 0, 0};
+    uint32_t ow[NWD], kw[NWD];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int v = 0; v < NWD; ++v) ow[v] = kw[v] = 0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
       const uint32_t c = (cw[j >> 2] >> (8 * (j & 3))) & 0xffu;
       const uint32_t nc = (uint32_t)fix_code<DT>(sgd_value<DT>(c, i0 + j, gv[j], lr, scale, minv), scale, minv) & 0xffu;
       ow[j >> 2] |= nc << (8 * (j & 3));
       if constexpr (has_kcopy<DT>()) kw[j >> 2] |= (uint32_t)kcode<DT>(nc) << (8 * (j & 3));
     }
-    *(uint4 *)(body + i0) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
-    if constexpr (has_kcopy<DT>()) *(uint4 *)(kbody + i0) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+    if constexpr (G == 16) {
+      *(uint4 *)(body + i0) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      if constexpr (has_kcopy<DT>()) *(uint4 *)(kbody + i0) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+    } else {
+      *(uint32_t *)(body + i0) = ow[0];
+      if constexpr (has_kcopy<DT>()) *(uint32_t *)(kbody + i0) = kw[0];
+    }
   }
-  const int64_t i = groups * 16 + threadIdx.x;
+  const int64_t i = groups * G + threadIdx.x;
   if (blockIdx.x == 0 && i < n) {
     const uint32_t nc = (uint32_t)fix_code<DT>(sgd_value<DT>(body[i], i, g[i], lr, scale, minv), scale, minv) & 0xffu;
     if constexpr (has_kcopy<DT>()) kbody[i] = kcode<DT>(nc);
@@ -453,8 +467,12 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
   }
 #define WH_SGD(D)                                                                           \
   if constexpr (dtype_bits(D) == 8 && fix_bytes<D>() == 1) {                               \
-    sgd8_kernel<D><<<grid_for(n / 16 + 1), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, \
-                                                            stop, bad, bad_value);          \
+    if (n >= ((int64_t)4 << 20))                                                            \
+      sgd8_kernel<D, 16><<<grid_for(n / 16 + 1), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, \
+                                                                  stop, bad, bad_value);    \
+    else /* small stores: four codes per thread, four times the threads */                \
+      sgd8_kernel<D, 4><<<grid_for(n / 4 + 1), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, \
+                                                                stop, bad, bad_value);      \
     return hipGetLastError();                                                               \
   } else if constexpr (D != kFloat32 && D != kFloat64) {                                    \
     sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
