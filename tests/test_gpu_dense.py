@@ -261,6 +261,37 @@ def test_e5m2_nonfinite_weights(oracle, batch):
     assert_close(np.where(fin, pre, 0), np.where(fin, rpre, 0), 256, "finite outputs")
 
 
+@pytest.mark.parametrize("shape", [(96, 512), (96, 2560)])
+@pytest.mark.parametrize("batch", [1, 3, 8, 40, 64])
+@pytest.mark.parametrize("dtype", [4, 26, 16, 9], ids=lambda d: DTYPE_NAMES[d])
+def test_nonfinite_inputs(oracle, dtype, batch, shape):
+    """Inf and NaN inputs through every forward route (GEMV, the split-x
+    GEMMs with and without a k split): NaN and Inf outputs where the f64
+    reference has them, with the same signs, including a NaN whose payload
+    sits only in the low 16 bits (its leading bf16 part reads as an
+    infinity); finite outputs within tolerance."""
+    rng = np.random.default_rng(1700 + dtype + batch + shape[1])
+    out, inn = shape
+    W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+    if dtype == 16:
+        W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+    x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+    low_nan = np.array([0x7F800001], np.uint32).view(np.float32)[0]
+    planted = [np.inf, -np.inf, np.nan, low_nan]
+    for i, v in enumerate(planted):
+        if i < batch:
+            x[i, (37 * i + 5) % inn] = v
+    Wd = oracle_weights(oracle, dtype, W)
+    pre, _ = pywelvet.forward(W, x, act=-1, dtype=dtype)
+    rpre, _ = oracle.forward(Wd, x, -1, None)
+    assert not np.all(np.isfinite(rpre))
+    np.testing.assert_array_equal(np.isnan(pre), np.isnan(rpre))
+    inf = np.isinf(rpre)
+    np.testing.assert_array_equal(np.where(inf, pre, 0), np.where(inf, rpre, 0))
+    fin = np.isfinite(rpre)
+    assert_close(np.where(fin, pre, 0), np.where(fin, rpre, 0), inn, "finite outputs")
+
+
 @pytest.mark.parametrize("batch", [5, 40])
 def test_backward_e5m2_nonfinite_weights(oracle, batch):
     """dX through an E5M2 store holding Inf and NaN codes keeps the IEEE

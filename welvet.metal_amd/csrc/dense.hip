@@ -1233,7 +1233,9 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
     }
   };
   // x = hi + mid + lo exactly: truncations to the top 8 significand bits,
-  // remainders exact in f32 (a non-finite x keeps its value in hi)
+  // remainders exact in f32; an infinite x keeps its value in hi (the
+  // remainders are zero), a NaN carries NaN into the remainders (its hi can
+  // read as an infinity when the payload sits in the low 16 bits)
   auto store_x = [&](int buf, const float (&xf)[XE], uint32_t in_mask) {
     uint32_t wp[3][XE / 2];
 #pragma unroll
@@ -1243,7 +1245,7 @@ __global__ void __launch_bounds__(256) gemm_bf3_kernel(GemmArgs a) {
       for (int e = 0; e < 2; ++e) {
         const float v = u2f(f2u(xf[i + e]) & in_mask);
         const uint32_t hi = f2u(v) & 0xffff0000u;
-        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const float r = isinf(v) ? 0.0f : v - u2f(hi);
         const uint32_t mid = f2u(r) & 0xffff0000u;
         part[0][e] = hi;
         part[1][e] = mid;
@@ -1436,7 +1438,7 @@ __global__ void __launch_bounds__(512) gemm_bf3k_kernel(GemmArgs a) {
       for (int e = 0; e < 2; ++e) {
         const float v = u2f(f2u(xf[i + e]) & in_mask);
         const uint32_t hi = f2u(v) & 0xffff0000u;
-        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const float r = isinf(v) ? 0.0f : v - u2f(hi);
         const uint32_t mid = f2u(r) & 0xffff0000u;
         part[0][e] = hi;
         part[1][e] = mid;
@@ -1656,7 +1658,7 @@ __global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
       for (int e = 0; e < 2; ++e) {
         const float v = u2f(f2u(xv[i + e]) & in_mask);
         const uint32_t hi = f2u(v) & 0xffff0000u;
-        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const float r = isinf(v) ? 0.0f : v - u2f(hi);
         const uint32_t mid = f2u(r) & 0xffff0000u;
         part[0][e] = hi;
         part[1][e] = mid;
@@ -1815,7 +1817,7 @@ __global__ void __launch_bounds__(512) gemm_bf3r_kernel(GemmArgs a, const double
       for (int e = 0; e < 2; ++e) {
         const float v = u2f(f2u(xv[i + e]) & in_mask);
         const uint32_t hi = f2u(v) & 0xffff0000u;
-        const float r = isfinite(v) ? v - u2f(hi) : 0.0f;
+        const float r = isinf(v) ? 0.0f : v - u2f(hi);
         const uint32_t mid = f2u(r) & 0xffff0000u;
         part[0][e] = hi;
         part[1][e] = mid;
