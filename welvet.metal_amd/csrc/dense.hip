@@ -1686,16 +1686,18 @@ __global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
   const int last = max(it, it_end - 1);
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    load_w(min(it + d, last), wr[d]);
     load_x(min(it + d, last), xf[d], xin[d]);
+    __builtin_amdgcn_sched_barrier(0);  // x before w, as in the loop (wait counts)
+    load_w(min(it + d, last), wr[d]);
   }
   store_x(0, xf[0], xin[0]);
-  __syncthreads();
+  lds_barrier();
   for (int u0 = it; u0 < it_end; u0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int u = u0 + d;
-      if (u >= it_end) break;
+      // leaving the whole loop keeps the ring's wait counts exact
+      if (u >= it_end) goto done;
       const int t = u / a.nst, st = u - t * a.nst;
       if (u == it || st == 0) {
 #pragma unroll
@@ -1713,8 +1715,8 @@ __global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
             bf3_weights<BK>(wr[d][c], q, t3, pp);
             bv[q][c][0] = pp[0];
           }
-        load_w(min(u + D, last), wr[d]);
         load_x(min(u + D, last), xf[d], xin[d]);
+        load_w(min(u + D, last), wr[d]);
 #pragma unroll
         for (int q = 0; q < 2; ++q) mfma_step(acc, buf, q, bv[q]);
       } else {
@@ -1729,7 +1731,7 @@ __global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
         load_w(min(u + D, last), wr[d]);
       }
       store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
-      __syncthreads();
+      lds_barrier();  // the next units' loads stay in flight
       buf ^= 1;
       if (st == a.nst - 1 || u + 1 == it_end) {
         // rows 4 g .. 4 g + 3 of the tile; a group wholly past M is never read
@@ -1743,6 +1745,7 @@ __global__ void __launch_bounds__(256) gemm_bf3s_kernel(GemmArgs a) {
       }
     }
   }
+done:;
 }
 
 // The split-x GEMM for batch <= 16 with no k split across workgroups: a
@@ -2628,6 +2631,7 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
 #define WH_GB(BK, D1)                                                                 \
   if (p.bm == 16) {                                                                   \
     if (p.bn == 128) gemm_bf3s_kernel<BK, D1, 1><<<p.blocks, 256, 0, s>>>(a);          \
+    else if (dep >= 3) gemm_bf3s_kernel<BK, 4, 2><<<p.blocks, 256, 0, s>>>(a);         \
     else if (dep == 2 || D1 == 2) gemm_bf3s_kernel<BK, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
     else gemm_bf3s_kernel<BK, 1, 2><<<p.blocks, 256, 0, s>>>(a);                       \
   } else if (p.bm == 32) {                                                            \
