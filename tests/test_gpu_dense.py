@@ -184,6 +184,32 @@ def test_split_x_small_batch_tile(oracle, dtype, batch):
                 pywelvet.set_tuning(k, v)
 
 
+@pytest.mark.parametrize("dtype", range(34), ids=DTYPE_NAMES)
+def test_small_batch_no_split_gemm(oracle, dtype):
+    """Batch <= 16 forwards with K <= 2048 on the no-split GEMM (fp32 MFMA
+    16x16x4 for the fp32-MFMA formats, the 16-row split-x GEMM for the
+    others): ragged N (70 and 1000 rows), K of 2.5 stages (320), exactly at
+    the bound (2048) and a 1024^2 layer at batch 16, bias + activation, and
+    the same cases with the no-split route off and forced.  W ~ N(0, 1/K)
+    keeps pre of order 1, where a saturating activation's output is compared
+    at the scale its input has."""
+    rng = np.random.default_rng(1700 + dtype)
+    cases = [(70, 320, 5, -1), (1000, 2048, 16, 1), (1024, 1024, 16, 3), (70, 320, 13, 0)]
+    for knob in (1, 0, 2):
+        old = pywelvet.set_tuning("bf3_rows", knob)
+        try:
+            for out, inn, batch, act in cases:
+                W = rng.normal(0, inn ** -0.5, (out, inn)).astype(np.float32)
+                x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+                if dtype == 16:  # FP4 has no scale: weights on its grid, x scaled instead
+                    W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+                    x = (x / (3.5 * inn ** 0.5)).astype(np.float32)
+                bias = rng.normal(0, 0.1, out) if act >= 0 else None
+                check_forward(oracle, dtype, W, x, act=act, bias=bias)
+        finally:
+            pywelvet.set_tuning("bf3_rows", old)
+
+
 def test_every_gemv_shape_knob_launches(oracle):
     """Every (chunks per lane, rows per block) request, including ones with
     no kernel of their own, computes the forward (falls back, never skips)."""

@@ -224,6 +224,10 @@ template <int DT>
 __global__ void lut_kernel(float scale, float minv, float *lut) {
   const int c = threadIdx.x;
   if (c < (1 << dtype_bits(DT))) lut[c] = dec_code<DT>((uint64_t)c, scale, minv);
+  if constexpr (dtype_bits(DT) == 4) {  // byte c = codes (c & 15, c >> 4)
+    lut[kPairLut + 2 * c] = dec_code<DT>((uint64_t)(c & 15), scale, minv);
+    lut[kPairLut + 2 * c + 1] = dec_code<DT>((uint64_t)(c >> 4), scale, minv);
+  }
 }
 
 // op_native_sgd ops_storage.metal:924-958 with the f64 contract: each element

@@ -295,7 +295,39 @@ struct GemvArgs {
   const double *bias;
   int bias_len, act;
   float *pre, *post;
-  float tab16[16];  // first 16 decoded values (the whole table of a 4-bit format)
+};
+
+// A GEMV block's LDS decode table, in two steps around the weight loads:
+// load() before them (so the wait for the table covers no weight load) and
+// store() + lds_barrier() after they are issued.  Thread t < 64 of the block
+// copies float4 entries t and t + 64 of the store's table (the pair table for
+// FL4P: 128 entries; other tables have at most 64); the loads read clamped
+// in-range entries.  Two named registers, no array: an array here is placed
+// in LDS by the compiler.
+template <int F>
+struct TabCopy {
+  static constexpr int kFloats = FI<F>::kTable;
+  static constexpr int kQ = (kFloats + 3) / 4;
+  static_assert(kQ <= 128, "two float4 per thread cover the table");
+  float4 q0, q1;
+  __device__ void load(const float *lut, int tid) {
+    const float4 *src = (const float4 *)(FI<F>::kPair ? lut + kPairLut : lut);
+    q0 = src[min(tid & 63, kQ - 1)];
+    if constexpr (kQ > 64) q1 = src[min((tid & 63) + 64, kQ - 1)];
+  }
+  __device__ void store(float *tab, int tid) const {
+    if (tid < 64 && tid < kQ) put(tab, tid, q0);
+    if constexpr (kQ > 64)
+      if (tid < 64 && tid + 64 < kQ) put(tab, tid + 64, q1);
+  }
+  __device__ static void put(float *tab, int i, float4 v) {
+    if constexpr (kFloats % 4 == 0) {
+      ((float4 *)tab)[i] = v;
+    } else {  // tables of 2 floats (1-bit formats)
+      if (4 * i < kFloats) tab[4 * i] = v.x;
+      if (4 * i + 1 < kFloats) tab[4 * i + 1] = v.y;
+    }
+  }
 };
 
 // ----------------------------------------------------------------- GEMV
@@ -525,29 +557,13 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
   using I = FI<F>;
   using Acc = std::conditional_t<F == FF64, double, float>;
   constexpr int E = I::kE, W = I::kW, NL = I::kTable;
-  __shared__ float lut_s[NL];
+  __shared__ __align__(16) float lut_s[NL];
   __shared__ double part[4][R];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  float lut_v = 0.0f;
-  if constexpr (F == FL4 || F == FL4P) {
-    // the 16 decoded values come in the kernel arguments (scalar registers),
-    // so filling the LDS table waits for no vector load
-    for (int b = tid; b < (F == FL4 ? 16 : 256); b += blockDim.x) {
-      float lo = a.tab16[0], hi = a.tab16[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        lo = (b & 15) == i ? a.tab16[i] : lo;
-        hi = (b >> 4) == i ? a.tab16[i] : hi;
-      }
-      if constexpr (F == FL4) lut_s[b] = lo;
-      else {
-        lut_s[2 * b] = lo;
-        lut_s[2 * b + 1] = hi;
-      }
-    }
-    __syncthreads();
-  } else if constexpr (I::kLut) {
-    if (tid < NL) lut_v = a.lut[tid];
+  TabCopy<F> tab;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before x and the weights
   }
   const int r0 = blockIdx.x * R;
   const int cbase = wave * 64 * C + lane;
@@ -573,10 +589,9 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
       load_words<W>(a.body + row * a.row_bytes + (int64_t)c * (W * 4), w[r][cc]);
     }
   }
-  if constexpr (I::kLut && F != FL4 && F != FL4P) {
-    if (tid < NL) lut_s[tid] = lut_v;
-    for (int i = tid + blockDim.x; i < NL; i += blockDim.x) lut_s[i] = a.lut[i];
-    __syncthreads();
+  if constexpr (I::kLut) {
+    tab.store(lut_s, tid);
+    lds_barrier();
   }
   // A wave whose column slice runs past the row end zeroes, on its lanes
   // past the end (duplicate reads), x and — for formats with non-finite
@@ -648,31 +663,15 @@ __global__ void __launch_bounds__(256) gemv_loop_kernel(GemvArgs a) {
   constexpr int E = I::kE, W = I::kW, NL = I::kTable;
   constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
   static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
-  __shared__ float lut_s[NL];
+  __shared__ __align__(16) float lut_s[NL];
   __shared__ double part[2][4][R];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int S = blockDim.x >> 6;
   const int ngroups = (a.N + R - 1) / R;
-  float lut_v = 0.0f;
-  if constexpr (F == FL4 || F == FL4P) {
-    // the 16 decoded values come in the kernel arguments (scalar registers),
-    // so filling the LDS table waits for no vector load
-    for (int b = tid; b < (F == FL4 ? 16 : 256); b += blockDim.x) {
-      float lo = a.tab16[0], hi = a.tab16[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        lo = (b & 15) == i ? a.tab16[i] : lo;
-        hi = (b >> 4) == i ? a.tab16[i] : hi;
-      }
-      if constexpr (F == FL4) lut_s[b] = lo;
-      else {
-        lut_s[2 * b] = lo;
-        lut_s[2 * b + 1] = hi;
-      }
-    }
-    __syncthreads();
-  } else if constexpr (I::kLut) {
-    if (tid < NL) lut_v = a.lut[tid];
+  TabCopy<F> tab;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before x and the weights
   }
   const int cbase = wave * 64 * C + lane;
   // issue order matters: vmcnt retires in order, so the table and x loads go
@@ -714,10 +713,9 @@ __global__ void __launch_bounds__(256) gemv_loop_kernel(GemvArgs a) {
       }
     }
     if (first) {
-      if constexpr (I::kLut && F != FL4 && F != FL4P) {
-        if (tid < NL) lut_s[tid] = lut_v;
-        for (int i = tid + blockDim.x; i < NL; i += blockDim.x) lut_s[i] = a.lut[i];
-        __syncthreads();
+      if constexpr (I::kLut) {
+        tab.store(lut_s, tid);
+        lds_barrier();
       }
       if (ragged) {
 #pragma unroll
@@ -1066,6 +1064,110 @@ __global__ void __launch_bounds__(256) gemm_reg_kernel(GemmArgs a) {
         dst[m * kRegBN + wave * 32 + j] = acc[mt][r];
       }
     it += nseg;
+  }
+}
+
+// Small-batch forward GEMM without a k split across workgroups (batch <= 16,
+// K <= 2048) on the fp32 MFMA 16x16x4: weights decoded straight into
+// B-operand registers and x read from L2 straight into A-operand registers.
+// Lane (j, h) of a wave supplies row j of both operands (x row m0 + j, W row
+// n0 + j) for k slot h: its KR consecutive k of each stage, so MFMA step t
+// covers k = k0 + KR*h + t.  A wave owns a 16 x 16 output tile and walks
+// stages g, g + KG, ... (g = its wave group); the KG partial tiles are added
+// in f64, in group order, through LDS, and the epilogue (bias + activation,
+// pre and post) runs here: no partial tiles in memory, no reduction launch.
+// Loads are straight-line from clamped in-range addresses; values past K, N
+// or M are zeroed after decode.
+template <int F>
+struct RegrShape {
+  static constexpr int E = FI<F>::kE;
+  static constexpr int KR = E >= 8 ? 32 : 4 * E;  // k per lane per stage
+  static constexpr int NCH = KR / E;               // chunk loads per lane per stage
+  static constexpr int ST = 4 * KR;                // k per stage
+};
+
+template <int F, int KG>
+__global__ void __launch_bounds__(64 * KG) gemm_regr_kernel(GemmArgs a, const double *bias, int bias_len,
+                                                            int act, float *pre, float *post) {
+  using I = FI<F>;
+  using S = RegrShape<F>;
+  constexpr int E = S::E, W = I::kW, KR = S::KR, NCH = S::NCH, ST = S::ST;
+  typedef float floatx4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) float lut_s[I::kTable];
+  __shared__ float ex[KG - 1][4][64];
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int j = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  TabCopy<F> tab;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before the stage loads
+  }
+  const int mrow = min(m0 + j, a.M - 1), nrow = min(n0 + j, a.N - 1);
+  const bool mlive = m0 + j < a.M, nlive = n0 + j < a.N;
+  const float *xr = a.A + (int64_t)mrow * a.K;
+  const uint8_t *wr = a.body + (int64_t)nrow * a.row_bytes;
+  struct Stage {
+    uint32_t w[NCH][W];
+    float x[KR];
+  };
+  auto load = [&](Stage &st, int s) {
+    const int k0 = s * ST + KR * h;
+#pragma unroll
+    for (int q = 0; q < KR; q += 4) {
+      const float4 v = *(const float4 *)(xr + min(k0 + q, a.K - 4));
+      st.x[q] = v.x; st.x[q + 1] = v.y; st.x[q + 2] = v.z; st.x[q + 3] = v.w;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      load_words<W>(wr + (int64_t)(min(k0 + c * E, a.K - E) / E) * (W * 4), st.w[c]);
+  };
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](const Stage &st, int s) {
+    const int k0 = s * ST + KR * h;
+    float bv[KR];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const bool ok = nlive && k0 + c * E < a.K;
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        bv[c * E + e] = ok ? (float)chunk_value<F>(st.w[c], e, lut_s, a.scale, a.minv) : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < KR; ++t) {
+      const float xv = (mlive && k0 + (t & ~3) < a.K) ? st.x[t] : 0.0f;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv, bv[t], acc, 0, 0, 0);
+    }
+  };
+  // stage g first, then the next stage of the group is loaded (clamped to
+  // the last stage: in range, unused) while the current one computes
+  Stage cur, nxt;
+  load(cur, min(g, a.nst - 1));
+  if constexpr (I::kLut) {
+    tab.store(lut_s, tid);
+    lds_barrier();
+  }
+  for (int s = g; s < a.nst; s += KG) {
+    load(nxt, min(s + KG, a.nst - 1));
+    compute(cur, s);
+    cur = nxt;
+  }
+  // D[4h + r][j] of the tile: groups 1.. hand theirs to group 0
+  if (g > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ex[g - 1][r][lane] = acc[r];
+  }
+  lds_barrier();
+  if (g != 0) return;
+  const int n = n0 + j;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = m0 + 4 * h + r;
+    double sum = (double)acc[r];
+#pragma unroll
+    for (int q = 0; q < KG - 1; ++q) sum += (double)ex[q][r][lane];
+    if (a.post != 1.0f) sum *= (double)a.post;
+    if (m < a.M && n < a.N) bias_act_store(sum, n, bias, bias_len, act, pre, post, (int64_t)m * a.N + n);
   }
 }
 
@@ -2522,6 +2624,23 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     p.bf3 = true;
     return p;
   }
+  // batch <= 16 without a k split (gemm_regr_kernel): the same K bound as the
+  // split-x 16-row GEMM
+  const int rk = g_tune[kTuneBf3Rows];
+  if (M <= 16 && K % 4 == 0 && (rk == 2 || (rk == 1 && K <= 2048))) {
+    SkPlan p;
+    p.rows = true;
+    p.bm = p.bn = 16;
+    p.gx = (N + 15) / 16;
+    p.gy = (M + 15) / 16;
+    const int e = fmt_chunk_elems(f), st = 4 * (e >= 8 ? 32 : 4 * e);  // RegrShape<F>::ST
+    p.nst = (K + st - 1) / st;
+    p.per_block = p.nst;
+    p.blocks = p.gx * p.gy;
+    p.maxspan = 1;
+    p.ws_bytes = 0;
+    return p;
+  }
   if (reg_gemm_ok(f) && g_tune[kTuneRegGemm] != 0) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
     return plan_sk(M, K, N, M <= 32 ? 32 : 64, kRegBN, occ);
@@ -2692,8 +2811,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   }
   if (route == 1) {
     GemvArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, w.cols, w.rows, w.cols / fmt_chunk_elems(f),
-               row_bytes_of(w), bias, bias_len, act, pre, post, {}};
-    for (int i = 0; i < 16; ++i) a.tab16[i] = w.tab16[i];
+               row_bytes_of(w), bias, bias_len, act, pre, post};
     if (batch == 1 && g_tune[kTuneGemv1] == 1) {
       // (C, R): chunks per lane and rows per block.  Auto: the fewest chunks
       // per lane that cover a row with at most 4 waves, and 8 / C rows; for
@@ -2736,7 +2854,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
           if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
         }
 #define WH_PF(F)                                                                         \
-  if constexpr (F == FE4 || F == FE5 || F == FF4) {                                      \
+  if constexpr (F == FE4 || F == FE5 || F == FF4 || F == FL4P) {                         \
     if (blocks < ngroups) {                                                              \
       if (C == 1 && R == 4) gemv_loop_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);  \
       else if (C == 1 && R == 8) gemv_loop_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a); \
@@ -2799,6 +2917,13 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
     if (p.rows) return launch_bf3r<true>(p, bk, a, bias, bias_len, act, pre, post, s);
     const hipError_t e = launch_bf3(p, bk, a, s);
     if (e != hipSuccess) return e;
+  } else if (p.rows) {
+#define WH_GRR(F)                                                                                     \
+  gemm_regr_kernel<F, 8><<<dim3(p.gx, p.gy), 512, 0, s>>>(a, bias, bias_len, act, pre, post);          \
+  break;
+    WH_FMT_SWITCH(f, WH_GRR)
+#undef WH_GRR
+    return hipGetLastError();
   } else if (p.bn == kRegBN) {
 #define WH_GR(F)                                                                      \
   if constexpr (FI<F>::kBits <= 16) {                                                 \

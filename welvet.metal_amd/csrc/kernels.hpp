@@ -16,6 +16,13 @@ struct Stats {
   unsigned long long maxkey;
 };
 
+// The store's decode table (Store::lut, kLutFloats floats): the 2^bits
+// decoded values from float 0, and for 4-bit formats the 256 byte-pair
+// entries {value of the low nibble, value of the high nibble} from float
+// kPairLut on, so a block copies its pair table instead of building it.
+constexpr int kPairLut = 256;
+constexpr int kLutFloats = kPairLut + 512;
+
 // Resident weight matrix: rows = out, cols = in (native_codec.cpp:112-136
 // bitstream order, header split off into minv).
 struct DevStore {
@@ -26,8 +33,7 @@ struct DevStore {
   float minv;
   const uint8_t *body;
   const uint8_t *kbody;  // FP8 formats: decode-ready copy of body (codec.hpp kcode)
-  const float *lut;  // 2^bits decoded values for formats of <= 8 bits
-  float tab16[16];   // host copy of the first 16 table values
+  const float *lut;  // decoded values for formats of <= 8 bits (layout: kPairLut)
   bool finite;       // no stored code decodes to Inf or NaN (known on the host)
   // codes of one byte (the decode-ready copy for FP8) transposed, [cols][rows],
   // for dX on the split-x GEMM; null when absent or stale

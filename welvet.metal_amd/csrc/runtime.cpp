@@ -184,9 +184,8 @@ welvet_status store_encode(Store *w, const float *d_w, bool repack, hipStream_t 
   w->minv = m.minv;
   w->finite = nonfinite == 0;
   if (dtype_lut(dtype)) {
-    if (w->lut == nullptr) WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
+    if (w->lut == nullptr) WH_HIP(hipMalloc(&w->lut, kLutFloats * sizeof(float)));
     WH_HIP(launch_lut(dtype, w->scale, w->minv, w->lut, s));
-    WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
     WH_HIP(hipStreamSynchronize(s));
   }
   return ok();
@@ -239,9 +238,8 @@ welvet_status store_from_native(Store *w, int dtype, int rows, int cols, float s
     WH_HIP(hipMemcpyAsync(w->kbody, k.data(), k.size(), hipMemcpyHostToDevice, s));
   }
   if (dtype_lut(dtype)) {
-    WH_HIP(hipMalloc(&w->lut, 256 * sizeof(float)));
+    WH_HIP(hipMalloc(&w->lut, kLutFloats * sizeof(float)));
     WH_HIP(launch_lut(dtype, w->scale, w->minv, w->lut, s));
-    WH_HIP(hipMemcpyAsync(w->tab16, w->lut, sizeof(w->tab16), hipMemcpyDeviceToHost, s));
   }
   WH_HIP(hipStreamSynchronize(s));  // k and the caller's buffers outlive the copies
   return ok();

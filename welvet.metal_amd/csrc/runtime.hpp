@@ -40,7 +40,6 @@ struct Store {
   double *bias = nullptr;
   int bias_len = 0;
 
-  float tab16[16] = {};  // host copy of the first 16 decoded table values
   // no code decodes to Inf / NaN: found at encode (FP8 E5M2 can hold them),
   // cleared by an SGD step of a format that can produce them
   bool finite = true;
@@ -49,9 +48,7 @@ struct Store {
   bool tbody_ok = false;
 
   DevStore dev() const {
-    DevStore d{dtype, rows, cols, scale, minv, body, kbody, lut, {}, finite, tbody_ok ? tbody : nullptr};
-    for (int i = 0; i < 16; ++i) d.tab16[i] = tab16[i];
-    return d;
+    return DevStore{dtype, rows, cols, scale, minv, body, kbody, lut, finite, tbody_ok ? tbody : nullptr};
   }
   int64_t n() const { return (int64_t)rows * cols; }
 };
