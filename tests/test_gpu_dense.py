@@ -206,6 +206,15 @@ def test_small_batch_no_split_gemm(oracle, dtype):
                     x = (x / (3.5 * inn ** 0.5)).astype(np.float32)
                 bias = rng.normal(0, 0.1, out) if act >= 0 else None
                 check_forward(oracle, dtype, W, x, act=act, bias=bias)
+                # dX through W^T on the same route family (rows = the
+                # reduction length), dW bit for bit
+                gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+                pre = rng.normal(0, 1, (batch, out)).astype(np.float32)
+                with pywelvet.Session(W, batch=batch, act=act, dtype=dtype) as s:
+                    dX, dW = s.backward(x, pre, gy)
+                _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, act)
+                assert_close(dX, rdX, out, f"{DTYPE_NAMES[dtype]} dX {out}x{inn} b{batch} rows={knob}")
+                assert_bit_equal(dW, rdW, f"{DTYPE_NAMES[dtype]} dW")
         finally:
             pywelvet.set_tuning("bf3_rows", old)
 

@@ -1171,6 +1171,143 @@ __global__ void __launch_bounds__(64 * KG) gemm_regr_kernel(GemmArgs a, const do
   }
 }
 
+// dX of the fp32-MFMA formats at batch <= 16, rows <= 2048, without a k
+// split: dX[b][i] = sum_o dpre[b][o] W[o][i] as gemm_regr_kernel's product
+// through W^T.  A wave owns 16 output columns i (n0..n0+15) and walks stages
+// of ST rows o of W; per stage its lanes load the 16-column piece of each row
+// as whole chunks along the row (the stored layout), decode it once into the
+// wave's own LDS tile (row pitch 17 floats: the four k slots of a read fall
+// on different banks), and MFMA step t reads B = tile[KR*h + t][j]; A is
+// dpre row j from L2 as in the forward.  The KG waves take every KG-th stage;
+// their tiles are added in f64 in wave order and stored as fl32.
+template <int F>
+struct RegtShape {
+  static constexpr int E = FI<F>::kE;
+  static constexpr int KR = E >= 4 ? 16 : 8;         // rows o per lane per stage
+  static constexpr int ST = 4 * KR;                   // rows per stage
+  static constexpr int CPR = E >= 16 ? 1 : 16 / E;    // chunks per 16-column row piece
+  static constexpr int NCH = ST * CPR / 64;           // chunk loads per lane per stage
+  static constexpr int DE = E >= 16 ? 16 : E;         // elements decoded per chunk load
+  static constexpr int P = 17;                        // tile row pitch (floats)
+  static_assert(ST * CPR % 64 == 0, "whole chunk loads per lane");
+};
+
+template <int F, int KG>
+__global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *out) {
+  using I = FI<F>;
+  using S = RegtShape<F>;
+  constexpr int E = S::E, W = I::kW, KR = S::KR, ST = S::ST, CPR = S::CPR, NCH = S::NCH, DE = S::DE,
+                P = S::P;
+  typedef float floatx4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) float lut_s[I::kTable];
+  __shared__ float tile[KG][ST * P];
+  __shared__ float ex[KG - 1][4][64];
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int j = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  TabCopy<F> tab;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before the stage loads
+  }
+  const int mrow = min(m0 + j, a.M - 1);
+  const bool mlive = m0 + j < a.M;
+  const float *xr = a.A + (int64_t)mrow * a.K;
+  // chunk load c of this lane: row r = q / CPR, chunk cc = q % CPR of the
+  // piece (q = lane + 64 c); column chunk index along the stored row
+  int lr[NCH], lcol[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int q = lane + 64 * c;
+    lr[c] = q / CPR;
+    lcol[c] = (q % CPR) * DE;  // first column of the piece this load decodes
+  }
+  const int64_t chunk_bytes = W * 4;
+  struct Stage {
+    uint32_t w[NCH][W];
+    float x[KR];
+  };
+  auto load = [&](Stage &st, int s) {
+    const int k0 = s * ST;
+#pragma unroll
+    for (int q = 0; q < KR; q += 4) {
+      const float4 v = *(const float4 *)(xr + min(k0 + KR * h + q, a.K - 4));
+      st.x[q] = v.x; st.x[q + 1] = v.y; st.x[q + 2] = v.z; st.x[q + 3] = v.w;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int o = min(k0 + lr[c], a.K - 1);
+      const int col = min(n0 + lcol[c], a.N - DE);
+      load_words<W>(a.body + (int64_t)o * a.row_bytes + (int64_t)(col / E) * chunk_bytes, st.w[c]);
+    }
+  };
+  // the decoded piece into this wave's tile; elements past K or N are zero.
+  // Sub-byte formats (32 per chunk) decode the half that holds n0..n0+15.
+  float *tw = tile[g];
+  auto put = [&](const Stage &st, int s) {
+    const int k0 = s * ST;
+    const bool hi = E == 32 && (n0 & 16);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const bool rok = k0 + lr[c] < a.K;
+#pragma unroll
+      for (int e = 0; e < DE; ++e) {
+        const bool ok = rok && n0 + lcol[c] + e < a.N;
+        float v;
+        if constexpr (E == 32)
+          v = hi ? (float)chunk_value<F>(st.w[c], 16 + e, lut_s, a.scale, a.minv)
+                 : (float)chunk_value<F>(st.w[c], e, lut_s, a.scale, a.minv);
+        else
+          v = (float)chunk_value<F>(st.w[c], e, lut_s, a.scale, a.minv);
+        tw[lr[c] * P + lcol[c] + e] = ok ? v : 0.0f;
+      }
+    }
+  };
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](const Stage &st, int s) {
+    const int k0 = s * ST + KR * h;
+#pragma unroll
+    for (int t = 0; t < KR; ++t) {
+      const float xv = (mlive && k0 + (t & ~3) < a.K) ? st.x[t] : 0.0f;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv, tw[(KR * h + t) * P + j], acc, 0, 0, 0);
+    }
+  };
+  Stage cur, nxt;
+  load(cur, min(g, a.nst - 1));
+  if constexpr (I::kLut) {
+    tab.store(lut_s, tid);
+    lds_barrier();
+  }
+  for (int s = g; s < a.nst; s += KG) {
+    load(nxt, min(s + KG, a.nst - 1));
+    // LDS operations of one wave complete in order: the previous stage's
+    // tile reads are done before these writes, and the writes before the
+    // reads below; the clobbers keep the compiler from reordering them
+    asm volatile("" ::: "memory");
+    put(cur, s);
+    asm volatile("" ::: "memory");
+    compute(cur, s);
+    asm volatile("" ::: "memory");
+    cur = nxt;
+  }
+  if (g > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ex[g - 1][r][lane] = acc[r];
+  }
+  lds_barrier();
+  if (g != 0) return;
+  const int n = n0 + j;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = m0 + 4 * h + r;
+    double sum = (double)acc[r];
+#pragma unroll
+    for (int q = 0; q < KG - 1; ++q) sum += (double)ex[q][r][lane];
+    if (a.post != 1.0f) sum *= (double)a.post;
+    if (m < a.M && n < a.N) out[(int64_t)m * a.N + n] = (float)sum;
+  }
+}
+
 // ------------------------------------------------------ split-x bf16 GEMM
 // For formats whose decoded weights are exact in bf16 once the per-tensor
 // scale is factored out (FP8 E4M3 from the decode-ready copy, Int8 codes),
@@ -2957,13 +3094,26 @@ int dx_route(const DevStore &w, int batch) {
 // dX of the GEMM route as a forward through W^T on the split-x GEMM: the
 // weight kinds of one byte per code whose transposed copy the store keeps
 // (-1 when dX takes the fp32 MFMA GEMM).
+bool dx_rows(const DevStore &w, int batch);
+
 int dx_bf3_kind(const DevStore &w, int batch) {
-  if (dx_route(w, batch) != 2 || w.rows % 16 != 0) return -1;
+  if (dx_route(w, batch) != 2 || w.rows % 16 != 0 || dx_rows(w, batch)) return -1;
   const int bk = bf3_kind(w);
   return (bk == BK_E4 || bk == BK_E5 || bk == BK_I8) ? bk : -1;
 }
 
 bool backward_wants_transposed(const DevStore &w, int batch) { return dx_bf3_kind(w, batch) >= 0; }
+
+// dX without a k split (gemm_regt_kernel, every format, no transposed copy):
+// batch <= 16 and the same rows bound as the forward's no-split GEMMs
+bool dx_rows(const DevStore &w, int batch) {
+  const int rk = g_tune[kTuneBf3Rows];
+  return dx_route(w, batch) == 2 && batch <= 16 && w.rows % 4 == 0 &&
+         (rk == 2 || (rk == 1 && w.rows <= 2048));
+}
+int dx_rows_stage(int f) {  // RegtShape<F>::ST
+  return 4 * (fmt_chunk_elems(f) >= 4 ? 16 : 8);
+}
 
 size_t backward_workspace_bytes(const DevStore &w, int batch) {
   const int route = dx_route(w, batch);
@@ -3034,6 +3184,15 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
       if (e != hipSuccess) return e;
       sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
     }
+  } else if (dx_rows(w, batch)) {
+    const int st = dx_rows_stage(f);
+    GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
+               (w.cols + 15) / 16, (batch + 15) / 16, (w.rows + st - 1) / st, 0, 1, nullptr, 16, 16};
+#define WH_DXR(F)                                                                 \
+  gemm_regt_kernel<F, 8><<<dim3(a.gx, a.gy), 512, 0, s>>>(a, dX);                 \
+  break;
+    WH_FMT_SWITCH(f, WH_DXR)
+#undef WH_DXR
   } else {
     const SkPlan p = plan_sk(batch, w.rows, w.cols);
     GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
