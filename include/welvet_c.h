@@ -353,9 +353,10 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      of the 32-row one [1]
  *   15 split-x GEMM on 8-wave workgroups whose two wave groups share each
  *      unit's k range (one partial tile per workgroup) [1]
- *   16 split-x GEMM for batch <= 16 with no k split across workgroups (32
- *      columns per workgroup over all of K, epilogue in the kernel): 0 off,
- *      1 for K <= 2048, 2 always [1] */
+ *   16 batch <= 16 forward and dX without a k split across workgroups
+ *      (epilogue in the kernel, no reduction launch; the split-x GEMM for
+ *      its formats, the fp32 MFMA for the others): 0 off, 1 for a
+ *      reduction length <= 2048, 2 always [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 /* No counterpart in the reference: a measurement aid.  Streams `bytes`

@@ -121,10 +121,11 @@ void set_forward_path(int path);
 // split-x GEMM's 16-row tile on the 16x16x32 MFMA for batch <= 16 (1 on).
 // 15 the split-x GEMM's two-group workgroups (8 waves sharing each unit's
 // k range, one partial tile per workgroup) for 32- and 64-row tiles of 256
-// columns when the k stages pair up (1 on).  16 for batch <= 16: the split-x
-// GEMM without a k split across workgroups (32 columns per workgroup over all
-// of K, four wave groups on alternate stages, epilogue in the kernel, no
-// reduction launch): 0 off, 1 for K <= 2048, 2 always.
+// columns when the k stages pair up (1 on).  16 for batch <= 16: forward and
+// dX without a k split across workgroups (gemm_bf3r_kernel for the split-x
+// formats' forward, gemm_regr_kernel for the others', gemm_regt_kernel for
+// every dX; epilogue in the kernel, no reduction launch): 0 off, 1 for a
+// reduction length <= 2048, 2 always.
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
