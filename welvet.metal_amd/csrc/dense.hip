@@ -2978,16 +2978,16 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         int R = 8 / C;
         const int rk = g_tune[kTuneGemvRows] ? g_tune[kTuneGemvRows] : Rauto;
         if (gemv_rows_knob(f) && gemv_pf_extra(C, rk)) R = rk;
-        // grid: one block per row group, or (knob / FP8, FP4 and pair-table
-        // default) a fixed number of waves per CU walking the row groups, x
-        // and the table loaded once each (others take one block per group;
-        // NF4 4096 -> 11008: 9.16 against 9.35 us, 4096^2 6.16 against 6.24)
+        // grid: one block per row group, or (knob / FP8 and FP4 default) a
+        // fixed number of waves per CU walking the row groups, x loaded once
+        // each (the hardware-converter formats; others take one block per
+        // group)
         const int ngroups = (a.N + R - 1) / R;
         int wpc = g_tune[kTuneGemvWaves];
         int blocks = ngroups;
         if (wpc < -1) blocks = (ngroups - wpc - 1) / -wpc;  // -k: k row groups per block
         else {
-          if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4 || f == FL4P) ? 16 : 0;
+          if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
           if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
         }
 #define WH_PF(F)                                                                         \

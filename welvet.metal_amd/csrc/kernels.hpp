@@ -110,8 +110,7 @@ void set_forward_path(int path);
 // 7 pair table for 4-bit formats (1 on).
 // 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
 // 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
-// block per row group; -1 = auto: 16 for the FP8 and FP4 converter formats and the
-// 4-bit pair-table formats,
+// block per row group; -1 = auto: 16 for the FP8 and FP4 converter formats,
 // else 0; -k for k >= 2: k row groups per block).
 // 10 split-x bf16 MFMA GEMM for FP8 E4M3 / E5M2, Int8, FP4 and NF4 (1 on), 11 its weight
 // prefetch depth in k stages (0 auto: 1, and 2 on two-group workgroups; 1, 2, or 3 for
