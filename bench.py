@@ -197,6 +197,96 @@ def cpu_baseline(dtypes=(4, 26), batch: int = 1, runs: int = 15):
                           "sample": "same steps, OpenMP over output rows"}}
 
 
+def cpu_config_baselines(runs: int = 5):
+    """BASELINE configs 2-5 on the host with the oracle's scalar port of the
+    reference host path (per-element decode switch, f64 dots, sequential fmaf
+    dW, fixed-scale re-encode SGD), the same shapes, seeds and weight
+    distributions as the GPU legs (inputs from numpy).  C2 / C3 forwards:
+    median of `runs` after one warm-up, on one thread at batch 1 (and C2's
+    batch 32) and on every host core the run may use at every batch.  C4: one
+    timed training step per dtype; C5: one timed step per dtype for all 34
+    (the GPU legs time 10 and 2; the oracle keeps no state between steps that
+    a warm-up would fill): the oracle's training kernels are OpenMP over the
+    host cores, so these report all cores."""
+    import numpy as np
+    from oracle import Oracle, Volume
+
+    O = Oracle()
+    ncores = min(16, len(os.sched_getaffinity(0)))
+    seed = 0x5EED0000
+    out = {"cores": ncores, "cpu_model": cpu_model(), "kind": "port"}
+
+    def med(fn, n):
+        fn()
+        t = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        return round(t[len(t) // 2] * 1e3, 3)
+
+    def chain(widths, dtype, init, rng):
+        return [O.pack(dtype, _weights(rng, widths[l + 1], widths[l], init)) for l in range(len(widths) - 1)]
+
+    def forward(widths, dtype, layers, x, threads):
+        for l, (raw, scale) in enumerate(layers):
+            _, x = O.forward_native(dtype, raw, scale, x, widths[l + 1], widths[l], -1, threads=threads)
+        return x
+
+    legs = [("c2", name, dt, [4096, 4096], "normal", b, seed + 1)
+            for name, dt in (("e4m3", 4), ("e5m2", 5)) for b in (1, 32)]
+    legs += [("c3", name, dt, [4096, 11008, 4096], init, b, seed + 2)
+             for name, dt, init in (("nf4", 26, "normal"), ("fp4_u6", 16, "uniform6")) for b in (1, 8, 64)]
+    cache = {}
+    for cfg, name, dt, widths, init, b, sd in legs:
+        key = (cfg, name)
+        if key not in cache:
+            cache[key] = chain(widths, dt, init, np.random.default_rng(sd))
+        layers = cache[key]
+        x = np.random.default_rng(sd + 100).standard_normal((b, widths[0]), dtype=np.float32)
+        leg = {"all_cores_ms": med(lambda: forward(widths, dt, layers, x, ncores), runs)}
+        if b == 1 or cfg == "c2":
+            leg["one_thread_ms"] = med(lambda: forward(widths, dt, layers, x, 1), runs)
+        tag = "x".join(map(str, widths)) if cfg == "c2" else "-".join(map(str, widths))
+        out[f"{cfg}_{name}_{tag}_b{b}"] = leg
+        print(f"# cpu {cfg} {name} b{b}: {leg}", file=sys.stderr, flush=True)
+
+    def train(dims, widths, dt, batch, sd):
+        rng = np.random.default_rng(sd)
+        D, R, Cc, L = dims
+        v = Volume(O, D, R, Cc, L, batch)
+        k = 0
+        for z in range(D):
+            for yy in range(R):
+                for xx in range(Cc):
+                    for l in range(L):
+                        W = _weights(rng, widths[k + 1], widths[k], "normal")
+                        v.bind_dense((z, yy, xx, l), W, act=-1 if k == len(widths) - 2 else 0, dtype=dt)
+                        k += 1
+        x = rng.standard_normal((batch, widths[0]), dtype=np.float32)
+        t = rng.standard_normal((batch, widths[-1]), dtype=np.float32)
+        return v, x, t
+
+    for name, dt in (("int8", 9), ("e4m3", 4)):
+        v, x, t = train((1, 1, 2, 1), [2048, 8192, 2048], dt, 256, seed + 3)
+        t0 = time.perf_counter()
+        v.train_step(x, t, 1e-3)
+        ms = (time.perf_counter() - t0) * 1e3
+        out[f"c4_{name}_2048-8192-2048_b256"] = {"all_cores_ms": round(ms, 3), "steps": 1}
+        print(f"# cpu c4 {name}: {ms:.1f} ms/step", file=sys.stderr, flush=True)
+    c5 = {}
+    for dt in range(34):
+        v, x, t = train((2, 2, 2, 4), [1024] * 33, dt, 16, seed + 4)
+        t0 = time.perf_counter()
+        v.train_step(x, t, 1e-3)
+        c5[pywelvet_name(dt)] = round((time.perf_counter() - t0) * 1e3, 3)
+    out["c5_2x2x2x4_1024_b16_all_cores_ms"] = c5
+    print(f"# cpu c5: {min(c5.values()):.1f}-{max(c5.values()):.1f} ms/step over 34 dtypes",
+          file=sys.stderr, flush=True)
+    return out
+
+
 # ---------------------------------------------------------------- configs
 # The other BASELINE configurations, reported under "config_results" (they
 # are not the headline metric).  Weights are seeded per config and layer.
@@ -392,6 +482,16 @@ def run_configs(torch, P, only=("c2", "c3", "c4", "c5")):
         for b in (1, 32):
             out[f"c2_{name}_4096x4096_b{b}"] = time_volume_forward(
                 torch, P, [4096, 4096], dt, b, 100, FWD_WARMUP, seed + 1)
+    if "c2" in only:
+        # the batch-1 legs against one launch's read of the same 16.8 MB
+        fl = read_floor(torch, P, 4096 * 4096, 200, FWD_WARMUP)
+        out["c2_read_floor_4096x4096"] = {"us": round(fl["us"], 3), "gbs": round(fl["gbs"], 1),
+                                          "kernel": fl["kernel"]}
+        for name in ("e4m3", "e5m2"):
+            leg = out[f"c2_{name}_4096x4096_b1"]
+            leg["frac_of_read_floor"] = round(fl["us"] / (leg["ms_per_step"] * 1e3), 4)
+        print(f"# c2 read floor (16.8 MB): {fl['us']:.2f} us/launch  {fl['gbs']:.0f} GB/s",
+              file=sys.stderr, flush=True)
     for name, dt, init in (("nf4", 26, "normal"), ("fp4", 16, "normal"), ("fp4_u6", 16, "uniform6")) \
             if "c3" in only else ():
         for b in (1, 8, 64):
@@ -494,6 +594,9 @@ def main():
                     help="comma list of the BASELINE configs to run: c2,c3,c4,c5")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (for scaling HBM counters)")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="also time BASELINE configs 2-5 on the host with the oracle (a few "
+                         "minutes of CPU work; not in the default run)")
     ap.add_argument("--wire", action="store_true",
                     help="run only the wire tool's --bench framing (host buffers; not the headline)")
     a = ap.parse_args()
@@ -558,6 +661,8 @@ def main():
     if not a.no_cpu:
         first = 26 if prim["weight_dtype"] == "nf4" else 4
         line["cpu_baseline"] = cpu_baseline((first, 30 - first), prim["batch"])
+    if a.cpu_configs:
+        line["cpu_config_baselines"] = cpu_config_baselines()
     print(json.dumps(line), flush=True)
 
 
