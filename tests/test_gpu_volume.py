@@ -194,3 +194,46 @@ def test_step_errors_match_oracle(oracle):
         G.set_remote_link((0, 0, 2, 0), (0, 0, 0, 0))
         st, _, _ = G.train_step(np.ones((1, 4)), np.zeros((1, 2)), 0.1, status=True)
         assert (st.code, st.message.decode()) == (1, "dense: bwd shape mismatch")
+
+
+def test_device_forward_writes_the_callers_buffer(oracle):
+    """welvet_hip_volume_forward_device: the last layer writes the caller's
+    d_y itself; the bytes equal the host-pointer forward's, on repeated calls,
+    in place (d_y == d_x, where the output is copied after the layers run),
+    and a host forward afterwards is unchanged."""
+    from devmem import DeviceArray, Stream
+    from parity import assert_bit_equal
+
+    rng = np.random.default_rng(77)
+    st = Stream()
+    try:
+        for widths, dt in (([256, 256], 4), ([256, 384, 256], 26), ([128, 320, 192], 1)):
+            L, batch = len(widths) - 1, 3
+            spec = {(0, 0, l, 0): (rng.normal(0, 0.1, (widths[l + 1], widths[l])).astype(np.float32),
+                                   0 if l < L - 1 else 2, dt, rng.normal(0, 0.1, widths[l + 1]))
+                    for l in range(L)}
+            G, V = build(oracle, (1, 1, L, 1), batch, spec)
+            with G:
+                x = rng.normal(0, 1, (batch, widths[0])).astype(np.float32)
+                want = G.forward(x, widths[-1])
+                code, _, ry, _ = V.forward(x)
+                assert code == 0
+                assert_close(want, ry, max(widths), "host forward")
+                dx = DeviceArray(x.shape)
+                dx.upload(x)
+                dy = DeviceArray((batch, widths[-1]), fill=np.nan)
+                for _ in range(2):
+                    pywelvet.check(pywelvet.lib().welvet_hip_volume_forward_device(
+                        G.h, dx.ptr, widths[0], dy.ptr, widths[-1], st.h))
+                    st.sync()
+                    assert_bit_equal(dy.download(), want, f"device forward {widths}")
+                if widths[0] == widths[-1]:
+                    pywelvet.check(pywelvet.lib().welvet_hip_volume_forward_device(
+                        G.h, dx.ptr, widths[0], dx.ptr, widths[-1], st.h))
+                    st.sync()
+                    assert_bit_equal(dx.download(), want, f"in-place device forward {widths}")
+                assert_bit_equal(G.forward(x, widths[-1]), want, "host forward after")
+                dx.free()
+                dy.free()
+    finally:
+        st.close()

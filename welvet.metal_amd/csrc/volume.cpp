@@ -158,15 +158,18 @@ welvet_status plan_forward(Grid *g, const float *d_x, int in_width, int *out_wid
 }
 
 // Enqueues the planned forward on `s`.
-welvet_status run_forward(Grid *g, hipStream_t s) {
+// final_post (nullable): where the last tape entry writes its activation
+// instead of its cell's post buffer (then tape_output does not hold it).
+welvet_status run_forward(Grid *g, hipStream_t s, float *final_post = nullptr) {
   for (int idx : g->tape) {  // the kernel plans (and workspace) follow the tuning knobs
     welvet_status st = grow_ws(g, forward_workspace_bytes(g->cells[idx].W.dev(), g->batch));
     if (st.code) return st;
   }
   for (size_t i = 0; i < g->tape.size(); ++i) {
     Grid::Cell &c = g->cells[g->tape[i]];
+    float *post = final_post != nullptr && i + 1 == g->tape.size() ? final_post : c.post;
     WH_HIP(launch_forward(c.W.dev(), g->batch, g->tape_in[i], c.W.bias, c.W.bias_len, c.act, c.pre,
-                          c.post, g->ws, g->ws_bytes, s));
+                          post, g->ws, g->ws_bytes, s));
   }
   return ok();
 }
@@ -510,10 +513,17 @@ welvet_status welvet_hip_volume_forward_device(welvet_hip_grid *g, const float *
   if (out != out_w)
     return make_status(kInvalid, "runtime.forward: output width %d, volume gives %d", out, out_w);
   const hipStream_t s = (hipStream_t)stream;
-  st = run_forward(g, s);
+  // the last layer writes d_y itself (one copy command less per call) unless
+  // d_y overlaps that layer's input, which it still reads while writing
+  const Grid::Cell &last = g->cells[g->tape.back()];
+  const uintptr_t y0 = (uintptr_t)d_y, y1 = y0 + (size_t)g->batch * out * sizeof(float);
+  const uintptr_t i0 = (uintptr_t)g->tape_in.back(), i1 = i0 + (size_t)g->batch * last.in * sizeof(float);
+  const bool direct = y1 <= i0 || i1 <= y0;
+  st = run_forward(g, s, direct ? d_y : nullptr);
   if (st.code) return st;
-  WH_HIP(hipMemcpyAsync(d_y, tape_output(g), (size_t)g->batch * out * sizeof(float),
-                        hipMemcpyDeviceToDevice, s));
+  if (!direct)
+    WH_HIP(hipMemcpyAsync(d_y, tape_output(g), (size_t)g->batch * out * sizeof(float),
+                          hipMemcpyDeviceToDevice, s));
   return ok();
 }
 
