@@ -237,3 +237,44 @@ def test_device_forward_writes_the_callers_buffer(oracle):
                 dy.free()
     finally:
         st.close()
+
+
+@pytest.mark.parametrize("dtype", [1, 4, 26])
+@pytest.mark.parametrize("batch", [5, 16])
+def test_train_derivative_in_dx_epilogue(oracle, dtype, batch):
+    """The piecewise activation derivatives (ReLU, ReLU2, LeakyReLU hidden
+    layers) applied in the layer above's dX epilogue give the same losses and
+    stored bytes, bit for bit, as the separate derivative launch, and the
+    steps agree with the oracle."""
+    from parity import assert_bit_equal
+
+    rng = np.random.default_rng(2300 + 3 * dtype + batch)
+    widths = [96, 128, 128, 64, 48]
+    acts = [0, 6, 5, -1]
+    spec = {(0, 0, l, 0): (rng.normal(0, 0.15, (widths[l + 1], widths[l])).astype(np.float32),
+                           acts[l], dtype, None) for l in range(4)}
+    x = rng.normal(0, 1, (batch, widths[0])).astype(np.float32)
+    t = rng.normal(0, 1, (batch, widths[-1])).astype(np.float32)
+    runs = {}
+    for fold in (1, 0):
+        old = pywelvet.set_tuning("fold_deriv", fold)
+        try:
+            G, V = build(oracle, (1, 1, 4, 1), batch, spec)
+            with G:
+                losses = []
+                for step in range(2):
+                    loss, y = G.train_step(x, t, 1e-2)
+                    losses.append(loss)
+                    if fold:
+                        code, _, rloss, ry = V.train_step(x, t, 1e-2)
+                        assert code == 0
+                        assert rel_err(y, ry) <= 4 * 1e-5, (step, rel_err(y, ry))
+                        _check_weights(G, V, spec, f"fold step {step}")
+                        for co in spec:
+                            V.cells[co]["raw"] = G.native(co)[0].copy()
+                runs[fold] = (losses, {co: G.native(co)[0].copy() for co in spec})
+        finally:
+            pywelvet.set_tuning("fold_deriv", old)
+    assert runs[1][0] == runs[0][0], (runs[1][0], runs[0][0])
+    for co in spec:
+        assert_bit_equal(runs[1][1][co], runs[0][1][co], f"store {co}")

@@ -245,6 +245,19 @@ __device__ inline float act_value(float v, int act) {
   return v;
 }
 
+// act_prime of the piecewise activations (ReLU, ReLU2, LeakyReLU; 1 for
+// every other id): act_prime below returns these for those ids, so a kernel
+// that applies one of them in its epilogue gives act_deriv_kernel's bits.
+__host__ __device__ inline bool act_piecewise(int act) { return act == kReLU || act == kReLU2 || act == kLeakyReLU; }
+__device__ inline float act_prime_piecewise(float v, int act) {
+  switch (act) {
+  case kReLU: return v > 0 ? 1.0f : 0.0f;
+  case kReLU2: return v > 0 ? 2 * v : 0.0f;
+  case kLeakyReLU: return v > 0 ? 1.0f : 0.01f;
+  }
+  return 1.0f;
+}
+
 __device__ inline float act_prime(float v, int act) {
   const double x = (double)v;
   switch (act) {
@@ -267,11 +280,8 @@ __device__ inline float act_prime(float v, int act) {
     const double z = sigmoid64(x);
     return (float)(z * (1.0 - z));
   }
-  case kReLU: return v > 0 ? 1.0f : 0.0f;
-  case kReLU2: return v > 0 ? 2 * v : 0.0f;
-  case kLeakyReLU: return v > 0 ? 1.0f : 0.01f;
   }
-  return 1.0f;
+  return act_prime_piecewise(v, act);
 }
 
 // Forward epilogue (welvet_dense.metal:87-105): pre = fl32(sum); with a bias

@@ -1192,8 +1192,14 @@ struct RegtShape {
   static_assert(ST * CPR % 64 == 0, "whole chunk loads per lane");
 };
 
-template <int F, int KG>
-__global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *out) {
+// NEXT: out is the gy of the layer below in a chain, whose piecewise
+// activation's derivative is applied here: out = fl32(dX) * act'(next_pre)
+// (act_deriv_kernel's expression on the stored dX, so the same bits), so
+// that layer's backward needs no derivative launch.  next_pre is loaded with
+// the first stage, off the epilogue's critical path.
+template <int F, int KG, bool NEXT>
+__global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *out, const float *next_pre,
+                                                            int next_act) {
   using I = FI<F>;
   using S = RegtShape<F>;
   constexpr int E = S::E, W = I::kW, KR = S::KR, ST = S::ST, CPR = S::CPR, NCH = S::NCH, DE = S::DE,
@@ -1274,6 +1280,14 @@ __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *o
   };
   Stage cur, nxt;
   load(cur, min(g, a.nst - 1));
+  float np[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (NEXT) {
+    if (g == 0) {  // the storing wave's four outputs, clamped in range
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        np[r] = next_pre[(int64_t)min(m0 + 4 * h + r, a.M - 1) * a.N + min(n0 + j, a.N - 1)];
+    }
+  }
   if constexpr (I::kLut) {
     tab.store(lut_s, tid);
     lds_barrier();
@@ -1304,7 +1318,9 @@ __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *o
 #pragma unroll
     for (int q = 0; q < KG - 1; ++q) sum += (double)ex[q][r][lane];
     if (a.post != 1.0f) sum *= (double)a.post;
-    if (m < a.M && n < a.N) out[(int64_t)m * a.N + n] = (float)sum;
+    float v = (float)sum;
+    if constexpr (NEXT) v = v * act_prime_piecewise(np[r], next_act);
+    if (m < a.M && n < a.N) out[(int64_t)m * a.N + n] = v;
   }
 }
 
@@ -2617,7 +2633,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -3131,15 +3147,23 @@ size_t backward_workspace_bytes(const DevStore &w, int batch) {
   return 0;
 }
 
+bool backward_dx_applies_next(const DevStore &w, int batch, int next_act) {
+  return g_tune[kTuneFoldDeriv] != 0 && act_piecewise(next_act) && dx_rows(w, batch);
+}
+
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre_buf, float *dX, float *dW, int *flag,
-                           void *ws, size_t ws_bytes, hipStream_t s) {
+                           void *ws, size_t ws_bytes, hipStream_t s, const BackwardChain &chain) {
   const int64_t ny = (int64_t)batch * w.rows;
   // dpre = gy * act'(pre); act' is 1 for Linear (and the ids act_prime
-  // treats as Linear), where gy * 1 = gy bit for bit: the kernel is skipped
+  // treats as Linear), where gy * 1 = gy bit for bit: the kernel is skipped,
+  // as it is when the layer above formed dpre in its dX epilogue
   const bool identity = act < kReLU || act > kReLU2;
-  const float *dpre = identity ? gy : dpre_buf;
-  if (!identity) act_deriv_kernel<<<blocks_for(ny), 256, 0, s>>>(gy, pre, ny, act, dpre_buf);
+  const float *dpre = identity || chain.gy_is_dpre ? gy : dpre_buf;
+  if (!identity && !chain.gy_is_dpre)
+    act_deriv_kernel<<<blocks_for(ny), 256, 0, s>>>(gy, pre, ny, act, dpre_buf);
+  if (chain.dx_next_pre != nullptr && (dX == nullptr || !backward_dx_applies_next(w, batch, chain.dx_next_act)))
+    return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int route = dx_route(w, batch);
@@ -3188,8 +3212,12 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     const int st = dx_rows_stage(f);
     GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
                (w.cols + 15) / 16, (batch + 15) / 16, (w.rows + st - 1) / st, 0, 1, nullptr, 16, 16};
-#define WH_DXR(F)                                                                 \
-  gemm_regt_kernel<F, 8><<<dim3(a.gx, a.gy), 512, 0, s>>>(a, dX);                 \
+#define WH_DXR(F)                                                                                   \
+  if (chain.dx_next_pre != nullptr)                                                                 \
+    gemm_regt_kernel<F, 8, true><<<dim3(a.gx, a.gy), 512, 0, s>>>(a, dX, chain.dx_next_pre,          \
+                                                                  chain.dx_next_act);               \
+  else                                                                                              \
+    gemm_regt_kernel<F, 8, false><<<dim3(a.gx, a.gy), 512, 0, s>>>(a, dX, nullptr, -1);              \
   break;
     WH_FMT_SWITCH(f, WH_DXR)
 #undef WH_DXR

@@ -76,9 +76,21 @@ hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *o
 bool backward_wants_transposed(const DevStore &w, int batch);
 // dpre = gy * act'(pre); dX = dpre . W (skipped when dX is null); dW =
 // sum_b dpre^T x (sequential FMA); flag |= 1 when dW holds a non-finite value.
+// A backward inside a chain of layers (the volume runtime's reverse walk):
+// gy_is_dpre: gy already holds dpre (the layer above applied this layer's
+// derivative in its dX epilogue), so no derivative launch; dx_next_pre /
+// dx_next_act: dX becomes the layer below's dpre, fl32(dX) * act'(pre of the
+// layer below), allowed only where backward_dx_applies_next holds (else the
+// launch fails with hipErrorInvalidValue).
+struct BackwardChain {
+  bool gy_is_dpre = false;
+  const float *dx_next_pre = nullptr;
+  int dx_next_act = -1;
+};
+bool backward_dx_applies_next(const DevStore &w, int batch, int next_act);
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
-                           void *ws, size_t ws_bytes, hipStream_t s);
+                           void *ws, size_t ws_bytes, hipStream_t s, const BackwardChain &chain = {});
 // SwiGLU element-wise steps (op_swiglu): h = fl32(silu(gate) * up);
 // backward d_up = fl32(gh * silu(gate)), d_gate = fl32(gh * up * silu'(gate)).
 hipError_t launch_swiglu_fwd(const float *gate, const float *up, int64_t n, float *h, hipStream_t s);
@@ -125,12 +137,14 @@ void set_forward_path(int path);
 // dX without a k split across workgroups (gemm_bf3r_kernel for the split-x
 // formats' forward, gemm_regr_kernel for the others', gemm_regt_kernel for
 // every dX; epilogue in the kernel, no reduction launch): 0 off, 1 for a
-// reduction length <= 2048, 2 always.
+// reduction length <= 2048, 2 always.  17 in a volume training step, the
+// derivative of a piecewise activation applied in the epilogue of the layer
+// above's no-split dX instead of a launch of its own (1 on).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kNumTune = 17
+  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kNumTune = 18
 };
 int set_tuning(int key, int value);
 

@@ -207,7 +207,11 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   // The first entry's input gradient is computed only when the caller asks
   // for it (training::step_dense does not return it).  Each dW launch flags
   // its own non-finite values, which the SGD of that cell reads.
+  // Where the dX kernel allows it, a layer's dX epilogue also applies the
+  // piecewise activation derivative of the layer below it in the tape, whose
+  // backward then takes gy as dpre (one launch less per layer, same bits).
   const float *gy = g->d_gy;
+  bool gy_is_dpre = false;
   for (int i = (int)g->tape.size() - 1; i >= 0; --i) {
     Grid::Cell &c = g->cells[g->tape[i]];
     float *gx = i > 0 || grad_in ? g->gx[i & 1] : nullptr;
@@ -215,9 +219,19 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
       welvet_status st = store_prepare_backward(&c.W, g->batch, s);
       if (st.code) return st;
     }
+    BackwardChain chain;
+    chain.gy_is_dpre = gy_is_dpre;
+    if (i > 0) {
+      const Grid::Cell &below = g->cells[g->tape[i - 1]];
+      if (backward_dx_applies_next(c.W.dev(), g->batch, below.act)) {
+        chain.dx_next_pre = below.pre;
+        chain.dx_next_act = below.act;
+      }
+    }
     WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, g->dpre, gx, c.dW,
-                           g->d_flag + 2 + i, g->ws, g->ws_bytes, s));
+                           g->d_flag + 2 + i, g->ws, g->ws_bytes, s, chain));
     gy = gx;
+    gy_is_dpre = chain.dx_next_pre != nullptr;
   }
   if (grad_in)
     WH_HIP(hipMemcpyAsync(grad_in, g->gx[0],
