@@ -359,7 +359,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      reduction length <= 2048, 2 always [1]
  *   17 volume training steps: a piecewise activation's derivative (ReLU,
  *      ReLU2, LeakyReLU) applied in the epilogue of the layer above's
- *      no-split dX instead of a launch of its own [1] */
+ *      no-split dX instead of a launch of its own [1]
+ *   18 volume training steps: the SGD of consecutive cells of one dtype in
+ *      one launch (up to 16 cells), 0 = one launch per cell [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 /* No counterpart in the reference: a measurement aid.  Streams `bytes`

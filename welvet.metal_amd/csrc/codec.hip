@@ -6,6 +6,8 @@
 // (ops_storage.metal:924-958) with one-thread-per-unit HBM-streaming kernels.
 // A unit is the smallest group of elements that owns whole bytes, so no two
 // threads ever write the same byte.
+#include <algorithm>
+
 #include "codec.hpp"
 #include "kernels.hpp"
 
@@ -252,18 +254,17 @@ __device__ inline bool sgd_stopped(int *stop, const int *bad, int bad_value) {
   return stop != nullptr && *stop != 0;
 }
 
+// The SGD element loops below take their block index and block count as
+// arguments: one launch per store (the block grid) or one launch for several
+// stores (sgd_batch_kernel: blockIdx.y picks the store).
 template <int DT>
-__global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body,
-                                                       uint8_t *__restrict__ kbody, int64_t n,
-                                                       const float *__restrict__ g, double lr,
-                                                       float scale, float minv, int *stop,
-                                                       const int *bad, int bad_value) {
-  if (sgd_stopped(stop, bad, bad_value)) return;
+__device__ inline void sgd_units(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
+                                 const float *__restrict__ g, double lr, float scale, float minv,
+                                 int64_t blk, int64_t nblk) {
   constexpr int bits = dtype_bits(DT);
   constexpr int U = unit_elems<DT>();
   const int64_t units = (n + U - 1) / U;
-  for (int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x; u < units;
-       u += (int64_t)gridDim.x * kThreads) {
+  for (int64_t u = blk * kThreads + threadIdx.x; u < units; u += nblk * kThreads) {
     if constexpr (bits >= 8) {
       const uint64_t c = fix_code<DT>(sgd_value<DT>(load_code<DT>(body, u), u, g[u], lr, scale, minv),
                                       scale, minv);
@@ -298,21 +299,29 @@ __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ bod
   }
 }
 
+template <int DT>
+__global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body,
+                                                       uint8_t *__restrict__ kbody, int64_t n,
+                                                       const float *__restrict__ g, double lr,
+                                                       float scale, float minv, int *stop,
+                                                       const int *bad, int bad_value) {
+  if (sgd_stopped(stop, bad, bad_value)) return;
+  sgd_units<DT>(body, kbody, n, g, lr, scale, minv, blockIdx.x, gridDim.x);
+}
+
 // sgd_kernel for the one-byte formats, 16 elements per thread: one 16-byte
 // code load, four float4 gradient loads and 16-byte stores (of the
 // decode-ready copy too, for FP8); the first block's threads take the
 // n mod 16 tail.  The per-element arithmetic is sgd_kernel's.
 template <int DT, int G>
-__global__ void __launch_bounds__(kThreads) sgd8_kernel(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody,
-                                                        int64_t n, const float *__restrict__ g, double lr,
-                                                        float scale, float minv, int *stop, const int *bad,
-                                                        int bad_value) {
+__device__ inline void sgd8_units(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
+                                  const float *__restrict__ g, double lr, float scale, float minv,
+                                  int64_t blk, int64_t nblk) {
   static_assert(dtype_bits(DT) == 8 && fix_bytes<DT>() == 1, "one-byte codes");
   static_assert(G == 4 || G == 16, "elements per thread");
   constexpr int NWD = G / 4;  // code words per thread
-  if (sgd_stopped(stop, bad, bad_value)) return;
   const int64_t groups = n / G;
-  for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < groups; q += (int64_t)gridDim.x * kThreads) {
+  for (int64_t q = blk * kThreads + threadIdx.x; q < groups; q += nblk * kThreads) {
     const int64_t i0 = q * G;
     uint32_t cw[NWD];
     if constexpr (G == 16) {
@@ -346,35 +355,84 @@ __global__ void __launch_bounds__(kThreads) sgd8_kernel(uint8_t *__restrict__ bo
     }
   }
   const int64_t i = groups * G + threadIdx.x;
-  if (blockIdx.x == 0 && i < n) {
+  if (blk == 0 && i < n) {
     const uint32_t nc = (uint32_t)fix_code<DT>(sgd_value<DT>(body[i], i, g[i], lr, scale, minv), scale, minv) & 0xffu;
     if constexpr (has_kcopy<DT>()) kbody[i] = kcode<DT>(nc);
     body[i] = (uint8_t)nc;
   }
 }
 
+template <int DT, int G>
+__global__ void __launch_bounds__(kThreads) sgd8_kernel(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody,
+                                                        int64_t n, const float *__restrict__ g, double lr,
+                                                        float scale, float minv, int *stop, const int *bad,
+                                                        int bad_value) {
+  if (sgd_stopped(stop, bad, bad_value)) return;
+  sgd8_units<DT, G>(body, kbody, n, g, lr, scale, minv, blockIdx.x, gridDim.x);
+}
+
 // Float64 storage keeps full f64: w = w - lr*g (native_codec.cpp:933-939
 // pinned to the f64 value its soft-double approximates).
+__device__ inline void sgd_f64_units(double *__restrict__ w, int64_t n, const float *__restrict__ g,
+                                     double lr, int64_t blk, int64_t nblk) {
+  for (int64_t i = blk * kThreads + threadIdx.x; i < n; i += nblk * kThreads) w[i] = w[i] - lr * (double)g[i];
+}
 __global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ w, int64_t n,
                                                            const float *__restrict__ g, double lr,
                                                            int *stop, const int *bad, int bad_value) {
   if (sgd_stopped(stop, bad, bad_value)) return;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads)
-    w[i] = w[i] - lr * (double)g[i];
+  sgd_f64_units(w, n, g, lr, blockIdx.x, gridDim.x);
 }
 
 // welvet_sgd_f32_f64_grad welvet_dense.metal:263-281: the step is rounded to
 // f32 first, then subtracted in f32.
+__device__ inline void sgd_f32_units(float *__restrict__ w, int64_t n, const float *__restrict__ g, double lr,
+                                     int64_t blk, int64_t nblk) {
+  for (int64_t i = blk * kThreads + threadIdx.x; i < n; i += nblk * kThreads) {
+    const float step = (float)(lr * (double)g[i]);
+    w[i] = w[i] - step;
+  }
+}
 __global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w, int64_t n,
                                                            const float *__restrict__ g, double lr,
                                                            int *stop, const int *bad, int bad_value) {
   if (sgd_stopped(stop, bad, bad_value)) return;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads) {
-    const float step = (float)(lr * (double)g[i]);
-    w[i] = w[i] - step;
+  sgd_f32_units(w, n, g, lr, blockIdx.x, gridDim.x);
+}
+
+// The SGD of up to kSgdBatch stores of one dtype in one launch (blockIdx.y =
+// store, blockIdx.x = block within it).  Every gradient was checked before
+// the launch (bad[k] != 0: store k's gradient holds a non-finite value), so
+// store c of the batch (index first + c in the sequence) is skipped when any
+// store k <= first + c is bad, exactly as a launch per store in sequence
+// order skips it; the first bad store records its code in *stop.  G: codes
+// per thread of the one-byte formats.
+template <int DT, int G>
+__global__ void __launch_bounds__(kThreads) sgd_batch_kernel(SgdBatch b, double lr, int *stop,
+                                                             const int *bad, int first) {
+  const int c = blockIdx.y;
+  if (c >= b.count) return;
+  const SgdStore &t = b.store[c];
+  // the first bad store up to this one: each lane reads one flag, a ballot
+  // finds the lowest set (one memory round trip per 64 stores)
+  const int upto = first + c, lane = threadIdx.x & 63;
+  int fb = -1;
+  for (int k0 = 0; k0 <= upto && fb < 0; k0 += 64) {
+    const int k = k0 + lane;
+    const uint64_t m = __ballot(k <= upto && bad[min(k, upto)] != 0);
+    if (m != 0) fb = k0 + __ffsll((unsigned long long)m) - 1;
   }
+  if (fb >= 0) {
+    if (fb == upto && blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(stop, 0, t.code);
+    return;
+  }
+  if (*stop != 0) return;
+  if constexpr (DT == kFloat32) sgd_f32_units((float *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
+  else if constexpr (DT == kFloat64) sgd_f64_units((double *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
+  else if constexpr (dtype_bits(DT) == 8 && fix_bytes<DT>() == 1)
+    sgd8_units<DT, G>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x);
+  else
+    sgd_units<DT>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x);
 }
 
 // flag := value when g holds a non-finite element and flag is still 0 (the
@@ -492,6 +550,30 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
 hipError_t launch_e5m2_nonfinite(const uint8_t *codes, int64_t n, int *flag, hipStream_t s) {
   e5m2_nonfinite_kernel<<<grid_for(n / 16 + 1), kThreads, 0, s>>>(codes, n, flag);
   return hipGetLastError();
+}
+
+hipError_t launch_sgd_batch(int dt, const SgdBatch &b, double lr, int *stop, const int *bad, int first,
+                            hipStream_t s) {
+  if (b.count < 1 || b.count > kSgdBatch || stop == nullptr || bad == nullptr) return hipErrorInvalidValue;
+  int64_t maxn = 0;
+  for (int i = 0; i < b.count; ++i) {
+    if (b.store[i].body == nullptr || b.store[i].g == nullptr || b.store[i].n < 0) return hipErrorInvalidValue;
+    if ((dt == kFP8E4M3 || dt == kFP8E5M2) && b.store[i].kbody == nullptr) return hipErrorInvalidValue;
+    maxn = std::max(maxn, b.store[i].n);
+  }
+#define WH_SGDB(D)                                                                                  \
+  if constexpr (dtype_bits(D) == 8 && fix_bytes<D>() == 1) {                                       \
+    if (maxn >= ((int64_t)4 << 20))                                                                 \
+      sgd_batch_kernel<D, 16><<<dim3(grid_for(maxn / 16 + 1), b.count), kThreads, 0, s>>>(b, lr, stop, bad, first); \
+    else                                                                                            \
+      sgd_batch_kernel<D, 4><<<dim3(grid_for(maxn / 4 + 1), b.count), kThreads, 0, s>>>(b, lr, stop, bad, first);   \
+  } else {                                                                                          \
+    const int64_t units = (D == kFloat32 || D == kFloat64) ? maxn : (maxn + unit_elems<D>() - 1) / unit_elems<D>(); \
+    sgd_batch_kernel<D, 4><<<dim3(grid_for(units), b.count), kThreads, 0, s>>>(b, lr, stop, bad, first); \
+  }                                                                                                 \
+  return hipGetLastError();
+  WH_DTYPE_SWITCH(dt, WH_SGDB)
+#undef WH_SGDB
 }
 
 hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s) {

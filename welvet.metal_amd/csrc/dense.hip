@@ -2633,7 +2633,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -2869,6 +2869,8 @@ int set_tuning(int key, int value) {
   g_tune[key] = value;
   return old;
 }
+
+int tuning(int key) { return key < 0 || key >= kNumTune ? -1 : g_tune[key]; }
 
 size_t forward_workspace_bytes(const DevStore &w, int batch) {
   if (fwd_route(w, batch) != 2) return 0;

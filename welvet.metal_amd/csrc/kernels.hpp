@@ -55,6 +55,26 @@ hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s
 hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
                       float scale, float minv, int *stop, const int *bad, int bad_value,
                       hipStream_t s);
+// The SGD of up to kSgdBatch stores of one dtype in one launch, as
+// launch_sgd on each in sequence: store c is skipped when bad[k] != 0 for any
+// k <= first + c (its own gradient or an earlier store's is non-finite), and
+// the first such store sets *stop = its code if *stop was 0.  The stores'
+// parameters travel in the kernel arguments.
+constexpr int kSgdBatch = 16;
+struct SgdStore {
+  uint8_t *body;
+  uint8_t *kbody;  // FP8 formats: the decode-ready copy (required), else null
+  const float *g;
+  int64_t n;
+  float scale, minv;
+  int code;  // the stop code when this store's gradient is the first non-finite one
+};
+struct SgdBatch {
+  SgdStore store[kSgdBatch];
+  int count;
+};
+hipError_t launch_sgd_batch(int dt, const SgdBatch &b, double lr, int *stop, const int *bad, int first,
+                            hipStream_t s);
 // *flag = value if g holds a non-finite element and *flag is still 0.
 hipError_t launch_nonfinite(const float *g, int64_t n, int *flag, int value, hipStream_t s);
 // *flag |= 1 if one of the n FP8 E5M2 codes is Inf or NaN (exponent field all ones).
@@ -139,13 +159,16 @@ void set_forward_path(int path);
 // every dX; epilogue in the kernel, no reduction launch): 0 off, 1 for a
 // reduction length <= 2048, 2 always.  17 in a volume training step, the
 // derivative of a piecewise activation applied in the epilogue of the layer
-// above's no-split dX instead of a launch of its own (1 on).
+// above's no-split dX instead of a launch of its own (1 on).  18 in a volume
+// training step, the SGD of consecutive stores of one dtype in one launch
+// (up to kSgdBatch per launch; 1 on, 0 one launch per store).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kNumTune = 18
+  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kNumTune = 19
 };
 int set_tuning(int key, int value);
+int tuning(int key);  // the current value (-1 for an unknown key)
 
 }  // namespace wh

@@ -243,21 +243,45 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   } else if (!std::isfinite(lr)) {
     late = make_status(kInvalid, "weights: bad SGD arguments");
   } else {
+    // Consecutive cells of one dtype share a launch (every dW and its flag
+    // exist by now, so a batch skips exactly the cells a launch per cell in
+    // this order would); a pending batch goes out before anything that
+    // stops the sequence.
+    const bool batched = tuning(kTuneSgdBatch) != 0;
+    SgdBatch batch{};
+    int batch_dt = -1, batch_first = 0;
+    auto flush = [&]() -> hipError_t {
+      if (batch.count == 0) return hipSuccess;
+      const hipError_t e = launch_sgd_batch(batch_dt, batch, lr, g->d_flag + 1, g->d_flag + 2, batch_first, s);
+      batch.count = 0;
+      return e;
+    };
     for (size_t j = 0; j < g->tape.size(); ++j) {
       Grid::Cell &c = g->cells[g->tape[j]];
       const int64_t n = c.W.n();
       const int code = c.W.dtype == kFloat32 ? kUnsupported : kInvalid;
       // the gradient check comes first, then the Float32 rate check (store_sgd order)
       if (c.W.dtype == kFloat32 && (std::fabs(lr) > FLT_MAX || std::fabs(lr) < FLT_MIN)) {
+        WH_HIP(flush());
         WH_HIP(launch_nonfinite(c.dW, n, g->d_flag + 1, code, s));
         late = make_status(kUnsupported, "SGD: learning rate outside the f32 range");
         break;
       }
-      WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv, g->d_flag + 1,
-                        g->d_flag + 2 + j, code, s));
+      if (batched) {
+        if (batch.count == kSgdBatch || (batch.count > 0 && batch_dt != c.W.dtype)) WH_HIP(flush());
+        if (batch.count == 0) {
+          batch_dt = c.W.dtype;
+          batch_first = (int)j;
+        }
+        batch.store[batch.count++] = SgdStore{c.W.body, c.W.kbody, c.dW, n, c.W.scale, c.W.minv, code};
+      } else {
+        WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv,
+                          g->d_flag + 1, g->d_flag + 2 + j, code, s));
+      }
       if (c.W.dtype == kFP8E5M2) c.W.finite = false;  // an update can overflow to Inf
       c.W.tbody_ok = false;
     }
+    WH_HIP(flush());
   }
   int stop = 0;
   double h_loss = 0.0;
