@@ -361,7 +361,10 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      ReLU2, LeakyReLU) applied in the epilogue of the layer above's
  *      no-split dX instead of a launch of its own [1]
  *   18 volume training steps: the SGD of consecutive cells of one dtype in
- *      one launch (up to 16 cells), 0 = one launch per cell [1] */
+ *      one launch (up to 16 cells), 0 = one launch per cell [1]
+ *   19 volume training steps: every layer's dW after the backward's dX
+ *      chain, up to 16 layers per launch (layers whose sizes are multiples
+ *      of 128), 0 = each with its layer's backward [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 /* No counterpart in the reference: a measurement aid.  Streams `bytes`

@@ -2478,14 +2478,14 @@ __global__ void __launch_bounds__(256) transpose_u8_kernel(const uint8_t *__rest
 // (batch rows 2s and 2s + 1) read opposite bank halves.  Rows past the batch
 // hold the -0 / 0 padding.  Same MFMA chain, so the same bits as
 // dw_mfma_kernel.
-__global__ void __launch_bounds__(256) dw_mfma_lds_kernel(const float *__restrict__ dpre,
-                                                          const float *__restrict__ x, int B, int rows,
-                                                          int cols, float *__restrict__ dW, int *flag) {
+// The 128 x 128 dW tile at block coordinates (bx, by).
+__device__ inline void dw_lds_tile(const float *__restrict__ dpre, const float *__restrict__ x, int B,
+                                   int rows, int cols, float *__restrict__ dW, int *flag, int bx, int by) {
   constexpr int kS = 16, kRow = 160;
   __shared__ float As[2][kS][kRow], Bs[2][kS][kRow];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int ob = blockIdx.y * 128, ib = blockIdx.x * 128;
+  const int ob = by * 128, ib = bx * 128;
   const int wo = (wave >> 1) * 64, wi = (wave & 1) * 64;
   // loader: thread t moves rows t / 32 and t / 32 + 8 of a panel, columns 4 (t % 32) .. + 3
   const int lr = tid >> 5, lc = (tid & 31) * 4;
@@ -2564,6 +2564,22 @@ __global__ void __launch_bounds__(256) dw_mfma_lds_kernel(const float *__restric
   if (flag != nullptr && __any(bad) && lane == 0) atomicOr(flag, 1);
 }
 
+__global__ void __launch_bounds__(256) dw_mfma_lds_kernel(const float *__restrict__ dpre,
+                                                          const float *__restrict__ x, int B, int rows,
+                                                          int cols, float *__restrict__ dW, int *flag) {
+  dw_lds_tile(dpre, x, B, rows, cols, dW, flag, blockIdx.x, blockIdx.y);
+}
+
+// The dW of up to kDwBatch layers in one launch (blockIdx.z = layer; the
+// grid covers the largest layer, blocks past a smaller one's tiles exit).
+__global__ void __launch_bounds__(256) dw_batch_kernel(DwBatch b) {
+  const int l = blockIdx.z;
+  if (l >= b.count) return;
+  const DwJob &t = b.job[l];
+  if ((int)blockIdx.x * 128 >= t.cols || (int)blockIdx.y * 128 >= t.rows) return;
+  dw_lds_tile(t.dpre, t.x, b.batch, t.rows, t.cols, t.dW, t.flag, blockIdx.x, blockIdx.y);
+}
+
 // ------------------------------------------------------------------ MSE
 __global__ void __launch_bounds__(256) mse_partial_kernel(const float *p, const float *t, int64_t n,
                                                           double *part) {
@@ -2633,7 +2649,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -3149,6 +3165,25 @@ size_t backward_workspace_bytes(const DevStore &w, int batch) {
   return 0;
 }
 
+bool dw_batchable(const DevStore &w) {
+  return g_tune[kTuneDwMfma] == 2 && w.rows % 128 == 0 && w.cols % 128 == 0;
+}
+
+hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s) {
+  if (b.count < 1 || b.count > kDwBatch || b.batch < 1) return hipErrorInvalidValue;
+  int gx = 0, gy = 0;
+  for (int i = 0; i < b.count; ++i) {
+    const DwJob &t = b.job[i];
+    if (t.dpre == nullptr || t.x == nullptr || t.dW == nullptr || t.rows % 128 || t.cols % 128 ||
+        t.rows < 128 || t.cols < 128)
+      return hipErrorInvalidValue;
+    gx = std::max(gx, t.cols / 128);
+    gy = std::max(gy, t.rows / 128);
+  }
+  dw_batch_kernel<<<dim3(gx, gy, b.count), 256, 0, s>>>(b);
+  return hipGetLastError();
+}
+
 bool backward_dx_applies_next(const DevStore &w, int batch, int next_act) {
   return g_tune[kTuneFoldDeriv] != 0 && act_piecewise(next_act) && dx_rows(w, batch);
 }
@@ -3238,7 +3273,12 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (g_tune[kTuneDwMfma] == 2 && w.rows % 128 == 0 && w.cols % 128 == 0) {
+  if (chain.dpre_out != nullptr) *chain.dpre_out = dpre;
+  if (chain.defer_dw) {
+    if (!dw_batchable(w)) return hipErrorInvalidValue;
+    return hipGetLastError();  // the caller launches this dW with others (launch_dw_batch)
+  }
+  if (dw_batchable(w)) {
     dim3 g2(w.cols / 128, w.rows / 128);
     dw_mfma_lds_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
   } else if (g_tune[kTuneDwMfma]) {

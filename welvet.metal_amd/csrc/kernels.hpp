@@ -102,12 +102,35 @@ bool backward_wants_transposed(const DevStore &w, int batch);
 // dx_next_act: dX becomes the layer below's dpre, fl32(dX) * act'(pre of the
 // layer below), allowed only where backward_dx_applies_next holds (else the
 // launch fails with hipErrorInvalidValue).
+// defer_dw: no dW launch (the caller batches it with launch_dw_batch, from
+// the dpre written to *dpre_out, which must stay intact until then); allowed
+// only where dw_batchable holds.
 struct BackwardChain {
   bool gy_is_dpre = false;
   const float *dx_next_pre = nullptr;
   int dx_next_act = -1;
+  bool defer_dw = false;
+  const float **dpre_out = nullptr;
 };
 bool backward_dx_applies_next(const DevStore &w, int batch, int next_act);
+// dW of up to kDwBatch layers in one launch, each as launch_backward computes
+// it (LDS-staged fp32 MFMA, sequential FMA over the batch; rows and columns
+// multiples of 128: dw_batchable), flag |= 1 per layer on a non-finite value.
+constexpr int kDwBatch = 16;
+struct DwJob {
+  const float *dpre;  // [batch][rows]
+  const float *x;     // [batch][cols]
+  int rows, cols;
+  float *dW;
+  int *flag;
+};
+struct DwBatch {
+  DwJob job[kDwBatch];
+  int count;
+  int batch;
+};
+bool dw_batchable(const DevStore &w);
+hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s);
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
                            void *ws, size_t ws_bytes, hipStream_t s, const BackwardChain &chain = {});
@@ -161,12 +184,14 @@ void set_forward_path(int path);
 // derivative of a piecewise activation applied in the epilogue of the layer
 // above's no-split dX instead of a launch of its own (1 on).  18 in a volume
 // training step, the SGD of consecutive stores of one dtype in one launch
-// (up to kSgdBatch per launch; 1 on, 0 one launch per store).
+// (up to kSgdBatch per launch; 1 on, 0 one launch per store).  19 in a
+// volume training step, the dW of every layer deferred to the end of the
+// backward and launched kDwBatch layers at a time (1 on).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kNumTune = 19
+  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kTuneDwBatch = 19, kNumTune = 20
 };
 int set_tuning(int key, int value);
 int tuning(int key);  // the current value (-1 for an unknown key)

@@ -32,6 +32,9 @@ struct welvet_hip_grid {
     int in = 0, out = 0, act = kLinear;
     Store W;
     float *pre = nullptr, *post = nullptr, *dW = nullptr;
+    // training: this cell's output gradient, then its dpre in place ([batch][out]),
+    // kept until the step's batched dW has read it
+    float *grad = nullptr;
   };
   std::mutex mu;
   int depth = 1, rows = 1, cols = 1, layers = 1, batch = 1;
@@ -72,9 +75,9 @@ welvet_status bad_coord(const char *which, int z, int y, int x, int l) {
 
 void free_cell(Grid::Cell *c) {
   free_store(&c->W);
-  for (float *p : {c->pre, c->post, c->dW})
+  for (float *p : {c->pre, c->post, c->dW, c->grad})
     if (p) (void)hipFree(p);
-  c->pre = c->post = c->dW = nullptr;
+  c->pre = c->post = c->dW = c->grad = nullptr;
   c->bound = false;
 }
 
@@ -210,11 +213,21 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   // Where the dX kernel allows it, a layer's dX epilogue also applies the
   // piecewise activation derivative of the layer below it in the tape, whose
   // backward then takes gy as dpre (one launch less per layer, same bits).
+  //
+  // With batched dW (knob on), each layer's dX goes to the cell below's grad
+  // buffer, the derivative is applied there in place, and the dW launches
+  // that allow it wait until the walk is done and run a batch at a time:
+  // the walk itself is then only the chain of dX launches.
+  const bool batch_dw = tuning(kTuneDwBatch) != 0;
+  DwBatch dwb{};
+  dwb.batch = g->batch;
   const float *gy = g->d_gy;
   bool gy_is_dpre = false;
   for (int i = (int)g->tape.size() - 1; i >= 0; --i) {
     Grid::Cell &c = g->cells[g->tape[i]];
-    float *gx = i > 0 || grad_in ? g->gx[i & 1] : nullptr;
+    float *gx = nullptr;
+    if (i > 0) gx = batch_dw ? g->cells[g->tape[i - 1]].grad : g->gx[i & 1];
+    else if (grad_in) gx = g->gx[0];
     if (gx != nullptr) {
       welvet_status st = store_prepare_backward(&c.W, g->batch, s);
       if (st.code) return st;
@@ -228,11 +241,22 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
         chain.dx_next_act = below.act;
       }
     }
-    WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, g->dpre, gx, c.dW,
-                           g->d_flag + 2 + i, g->ws, g->ws_bytes, s, chain));
+    const float *dpre = nullptr;
+    chain.defer_dw = batch_dw && dw_batchable(c.W.dev());
+    chain.dpre_out = &dpre;
+    WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, batch_dw ? c.grad : g->dpre,
+                           gx, c.dW, g->d_flag + 2 + i, g->ws, g->ws_bytes, s, chain));
+    if (chain.defer_dw) {
+      dwb.job[dwb.count++] = DwJob{dpre, g->tape_in[i], c.W.rows, c.W.cols, c.dW, g->d_flag + 2 + i};
+      if (dwb.count == kDwBatch) {
+        WH_HIP(launch_dw_batch(dwb, s));
+        dwb.count = 0;
+      }
+    }
     gy = gx;
     gy_is_dpre = chain.dx_next_pre != nullptr;
   }
+  if (dwb.count > 0) WH_HIP(launch_dw_batch(dwb, s));
   if (grad_in)
     WH_HIP(hipMemcpyAsync(grad_in, g->gx[0],
                           (size_t)g->batch * g->cells[g->tape[0]].in * sizeof(float),
@@ -303,6 +327,7 @@ welvet_status prepare_step(Grid *g, int out_width) {
     max_in = std::max<int64_t>(max_in, c.in);
     max_out = std::max<int64_t>(max_out, c.out);
     if (!c.dW) WH_HIP(hipMalloc(&c.dW, (size_t)c.W.n() * sizeof(float)));
+    if (!c.grad) WH_HIP(hipMalloc(&c.grad, (size_t)g->batch * c.out * sizeof(float)));
     welvet_status st = grow_ws(g, backward_workspace_bytes(c.W.dev(), g->batch));
     if (st.code) return st;
   }
