@@ -3169,6 +3169,15 @@ bool dw_batchable(const DevStore &w) {
   return g_tune[kTuneDwMfma] == 2 && w.rows % 128 == 0 && w.cols % 128 == 0;
 }
 
+// Deferring a layer's dW into a batched launch pays where the layer alone
+// leaves CUs idle (fewer 128x128 tiles than CUs: config 5's 1024^2 layers,
+// 64 tiles, 130-145 us less per step); a layer that fills the GPU runs alone
+// (config 4's 2048 x 8192 layers, 1024 tiles each: 50 us per step slower
+// batched).
+bool dw_defer_pays(const DevStore &w) {
+  return dw_batchable(w) && (int64_t)(w.rows / 128) * (w.cols / 128) < num_cus();
+}
+
 hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s) {
   if (b.count < 1 || b.count > kDwBatch || b.batch < 1) return hipErrorInvalidValue;
   int gx = 0, gy = 0;

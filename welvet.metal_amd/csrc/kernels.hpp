@@ -130,6 +130,7 @@ struct DwBatch {
   int batch;
 };
 bool dw_batchable(const DevStore &w);
+bool dw_defer_pays(const DevStore &w);  // batchable, and the layer alone leaves CUs idle
 hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s);
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,

@@ -215,9 +215,9 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   // backward then takes gy as dpre (one launch less per layer, same bits).
   //
   // With batched dW (knob on), each layer's dX goes to the cell below's grad
-  // buffer, the derivative is applied there in place, and the dW launches
-  // that allow it wait until the walk is done and run a batch at a time:
-  // the walk itself is then only the chain of dX launches.
+  // buffer, the derivative is applied there in place, and the dW launches of
+  // layers too small to fill the GPU wait until the walk is done and run a
+  // batch at a time: the walk is then only the chain of dX launches.
   const bool batch_dw = tuning(kTuneDwBatch) != 0;
   DwBatch dwb{};
   dwb.batch = g->batch;
@@ -242,7 +242,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
       }
     }
     const float *dpre = nullptr;
-    chain.defer_dw = batch_dw && dw_batchable(c.W.dev());
+    chain.defer_dw = batch_dw && dw_defer_pays(c.W.dev());
     chain.dpre_out = &dpre;
     WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, batch_dw ? c.grad : g->dpre,
                            gx, c.dW, g->d_flag + 2 + i, g->ws, g->ws_bytes, s, chain));
