@@ -239,6 +239,28 @@ def test_every_gemv_shape_knob_launches(oracle):
             pywelvet.set_tuning(k, v)
 
 
+@pytest.mark.parametrize("dtype", [4, 5, 16, 26])
+def test_loop_gemv_ragged_rows(oracle, dtype):
+    """The fixed-grid batch-1 GEMV (several row groups per block) for every
+    (chunks per lane, rows per block) it is built for, on row counts that
+    leave a partial last group and on blocks that walk 2 or 3 groups."""
+    rng = np.random.default_rng(29 + dtype)
+    names = ("cr", "gemv_rows", "gemv_waves")
+    old = {k: pywelvet.set_tuning(k, 0) for k in names}
+    try:
+        for cr, rows in ((3, 4), (3, 8), (3, 2), (1, 4)):
+            for waves in (-2, -3):
+                for k, v in zip(names, (cr, rows, waves)):
+                    pywelvet.set_tuning(k, v)
+                for out, inn in ((203, 4096), (11, 1024), (37, 2048)):
+                    W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+                    x = rng.normal(0, 1, (1, inn)).astype(np.float32)
+                    check_forward(oracle, dtype, W, x)
+    finally:
+        for k, v in old.items():
+            pywelvet.set_tuning(k, v)
+
+
 @pytest.mark.parametrize("dtype", [1, 2, 4, 9, 16, 26, 27, 33])
 def test_forward_ragged_shapes(oracle, dtype):
     """Columns that are not a whole number of chunks take the element-wise route."""

@@ -2990,6 +2990,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       // chunks per lane cover, 4 rows (measured best: more blocks in flight
       // for the heavier FP8 decode, one wave per block for 4-bit)
       int C = 1, Rauto = 0;
+      bool loop16 = false;
       switch (g_tune[kTuneCR]) {
       case 1: C = 2; break;
       case 2: C = 4; break;
@@ -3000,6 +3001,13 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         if ((f == FE4 || f == FE5 || f == FI8) && C == 1) Rauto = 4;
         if (f == FF4 && C == 1) Rauto = 8;
         if ((f == FL4P || f == FL4) && a.nchunks <= 128) C = 2, Rauto = 4;
+        // pair-table rows of at most two waves of one chunk per lane, with
+        // more 4-row groups than 16 waves per CU hold: one chunk per lane in
+        // the fixed-grid loop (measured at 4096 -> 11008: 8.90-8.96 against
+        // 9.22-9.30 us with two chunks per lane, one block per group)
+        if (f == FL4P && a.nchunks <= 128 &&
+            16 * num_cus() / ((a.nchunks + 63) / 64) < (a.N + 3) / 4)
+          C = 1, Rauto = 4, loop16 = true;
         // 4-bit rows that take three or more waves of two chunks per lane
         // (11008-wide inputs): 8 rows per block (measured at 11008 -> 4096:
         // FP4 8.2 against 9.1 us, NF4 10.2 against 10.6 us with 4)
@@ -3021,7 +3029,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         int blocks = ngroups;
         if (wpc < -1) blocks = (ngroups - wpc - 1) / -wpc;  // -k: k row groups per block
         else {
-          if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
+          if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4 || loop16) ? 16 : 0;
           if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
         }
 #define WH_PF(F)                                                                         \
