@@ -261,6 +261,30 @@ def test_loop_gemv_ragged_rows(oracle, dtype):
             pywelvet.set_tuning(k, v)
 
 
+@pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26])
+def test_batched_gemv(oracle, dtype):
+    """Batch 2-8 through the GEMV that holds x of every batch row in
+    registers: batches that fill and that pad its 2 / 4 / 8 register rows,
+    rows of one wave (1024 inputs), of a partial last wave (2080), of one and
+    two chunks per lane (4096, 11008), row counts that leave a partial last
+    group, and three grids (8, 4 and 16 waves per CU)."""
+    rng = np.random.default_rng(31 + dtype)
+    old = pywelvet.set_tuning("gemv_batch", 1)
+    try:
+        for knob in (1, 4, 16):
+            pywelvet.set_tuning("gemv_batch", knob)
+            for out, inn in ((203, 4096), (37, 1024), (11, 2080), (40, 11008)):
+                if dtype == 16:
+                    W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+                else:
+                    W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+                for batch in (2, 3, 4, 5, 8):
+                    x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+                    check_forward(oracle, dtype, W, x)
+    finally:
+        pywelvet.set_tuning("gemv_batch", old)
+
+
 @pytest.mark.parametrize("dtype", [1, 2, 4, 9, 16, 26, 27, 33])
 def test_forward_ragged_shapes(oracle, dtype):
     """Columns that are not a whole number of chunks take the element-wise route."""

@@ -770,6 +770,162 @@ __global__ void __launch_bounds__(256) gemv_loop_kernel(GemvArgs a) {
   for (int g = blockIdx.x; g < ngroups; g += gridDim.x, buf ^= 1) group(g, g == (int)blockIdx.x, buf);
 }
 
+// gemv_loop_kernel for batch 2..B: the block holds the column slice of x of
+// all B batch rows in registers, so each weight chunk is loaded and decoded
+// once and feeds B products.  A row group is R rows; its R * B sums (one fp32
+// FMA chain per row and batch row over the lane's C * E products) go through
+// the f64 butterfly as R * B rows, then the ordered f64 sum over the S slices.
+// Batch rows from `batch` to B - 1 read x row batch - 1 and are never stored.
+template <int F, int C, int R, int B>
+__global__ void __launch_bounds__(512) gemv_loopb_kernel(GemvArgs a, int batch) {
+  using I = FI<F>;
+  constexpr int E = I::kE, W = I::kW, NL = I::kTable, V = R * B;
+  constexpr int LV = V == 2 ? 1 : V == 4 ? 2 : V == 8 ? 3 : 4;
+  static_assert((1 << LV) == V, "rows per group times batch rows must be 2, 4, 8 or 16");
+  __shared__ __align__(16) float lut_s[NL];
+  __shared__ double part[2][8][V];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int S = blockDim.x >> 6;
+  const int ngroups = (a.N + R - 1) / R;
+  TabCopy<F> tab;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before x and the weights
+  }
+  const int cbase = wave * 64 * C + lane;
+  float xv[B][C][E];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const float *xb = a.x + (int64_t)min(b, batch - 1) * a.K;
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) {
+      const int c = min(cbase + cc * 64, a.nchunks - 1);
+      load_x<E>(xb + (int64_t)c * E, xv[b][cc]);
+    }
+  }
+  // lanes past the row end (duplicate reads) add exact zeros: x and, for
+  // formats with non-finite codes, the weight words are masked
+  const bool ragged = __builtin_amdgcn_readfirstlane(wave) * 64 * C + 64 * C > a.nchunks;
+  uint32_t keep[C];
+#pragma unroll
+  for (int cc = 0; cc < C; ++cc) {
+    keep[cc] = cbase + cc * 64 < a.nchunks ? ~0u : 0u;
+    asm volatile("" : "+v"(keep[cc]));
+  }
+  // one row group's weight loads (non-temporal: streamed once)
+  using Words = uint32_t[R][C][W];
+  auto load_group = [&](int g, Words &w) {
+    const int r0 = g * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = min(r0 + r, a.N - 1);
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc) {
+        const int c = min(cbase + cc * 64, a.nchunks - 1);
+        load_words_nt<W>(a.body + row * a.row_bytes + (int64_t)c * (W * 4), w[r][cc]);
+      }
+    }
+  };
+  // decode + FMA, reductions, epilogue of row group g from its loaded words
+  auto group = [&](int g, Words &w, int buf) {
+    const int r0 = g * R;
+    if constexpr (I::kMayBeNonFinite) {
+      if (ragged) {
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc)
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < W; ++i) w[r][cc][i] &= keep[cc];
+      }
+    }
+    double acc[V];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float sm[B];
+#pragma unroll
+      for (int b = 0; b < B; ++b) sm[b] = 0.0f;
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc) {
+        float v[E];
+        decode_chunk<F>(w[r][cc], v, lut_s, a.scale, a.minv);
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+#pragma unroll
+          for (int b = 0; b < B; ++b) sm[b] = fmaf(v[e], xv[b][cc][e], sm[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < B; ++b) acc[r * B + b] = (double)sm[b];
+    }
+    // lane l: the sum of (row, batch row) l >> (6 - LV) over the wave
+    const double v = row_reduce<V>(acc, lane);
+    if (S == 1) {
+      if ((lane & ((64 >> LV) - 1)) == 0) {
+        const int vr = lane >> (6 - LV), row = r0 + vr / B, b = vr % B;
+        if (row < a.N && b < batch)
+          bias_act_store(v, row, a.bias, a.bias_len, a.act, a.pre, a.post, (int64_t)b * a.N + row);
+      }
+      return;
+    }
+    // part is double-buffered: the next group's writes go to the other half,
+    // and the barrier of that group orders them after this group's reads
+    if ((lane & ((64 >> LV) - 1)) == 0) part[buf][wave][lane >> (6 - LV)] = v;
+    __syncthreads();
+    if (tid < V) {
+      const int row = r0 + tid / B, b = tid % B;
+      if (row < a.N && b < batch) {
+        double sum = 0;
+        for (int q = 0; q < S; ++q) sum += part[buf][q][tid];
+        bias_act_store(sum, row, a.bias, a.bias_len, a.act, a.pre, a.post, (int64_t)b * a.N + row);
+      }
+    }
+  };
+  // The block walks row groups blockIdx.x, + gridDim.x, ... (the grid never
+  // exceeds the group count).  From B = 4 on (at most 3 waves per SIMD) the
+  // next group's loads are in flight while it works on the current one, two
+  // word buffers alternating; past the last group that prefetch re-reads the
+  // last row group (every block the same rows), so the loads stay
+  // unconditional.  At B = 2 the extra buffer would cost occupancy instead.
+  constexpr bool kPrefetch = B >= 4;
+  Words wa, wb;
+  int g = blockIdx.x;
+  load_group(g, wa);
+  if constexpr (I::kLut) {
+    tab.store(lut_s, tid);
+    lds_barrier();
+  }
+  if (ragged) {
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc)
+#pragma unroll
+        for (int e = 0; e < E; ++e) xv[b][cc][e] = __uint_as_float(__float_as_uint(xv[b][cc][e]) & keep[cc]);
+  }
+  if constexpr (!kPrefetch) {
+    for (int buf = 0;; buf ^= 1) {
+      group(g, wa, buf);
+      g += gridDim.x;
+      if (g >= ngroups) break;
+      load_group(g, wa);
+    }
+    return;
+  }
+  // consecutive groups use opposite halves of part: 0 for wa, 1 for wb
+  for (;;) {
+    int gn = g + gridDim.x;
+    load_group(min(gn, ngroups - 1), wb);
+    group(g, wa, 0);
+    if (gn >= ngroups) break;
+    g = gn;
+    gn = g + gridDim.x;
+    load_group(min(gn, ngroups - 1), wa);
+    group(g, wb, 1);
+    if (gn >= ngroups) break;
+    g = gn;
+  }
+}
+
 // Element-wise fallback for shapes whose rows do not start on a chunk
 // boundary: a block per output row, f64 accumulation, any batch.
 template <int DT>
@@ -2649,7 +2805,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -2819,12 +2975,50 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
 
 constexpr int kDxSegRows = 32;
 
+// Batch 2-8 on gemv_loopb_kernel: B batch rows in registers (the batch
+// rounded up to 2, 4 or 8), C chunks per lane (1, else 2), S waves per
+// block covering the row (at most 8); false when x of B rows would take more
+// than 128 registers per lane or the row more than 8 waves, or for formats
+// without that kernel.
+struct GemvBatchShape {
+  int B, C, S;
+};
+bool gemv_batch_shape(int f, int batch, int nchunks, int rows, GemvBatchShape &sh) {
+  if (g_tune[kTuneGemvBatch] == 0 || batch < 2 || batch > 8) return false;
+  if (f != FE4 && f != FE5 && f != FI8 && f != FF4 && f != FL4P) return false;
+  const int E = fmt_chunk_elems(f);
+  const int B = batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
+  // 8 batch rows only up to 32 M weights (FP8 b8: 4096^2 12.3 against 15.8
+  // us on the split-x GEMM, 4096 x 11008 24.6 against 19.9)
+  if (B == 8 && (int64_t)rows * nchunks * E > ((int64_t)32 << 20)) return false;
+  for (int C = 1; C <= 2 && B * C * E <= 128; C *= 2) {
+    const int S = (nchunks + 64 * C - 1) / (64 * C);
+    if (S <= 8) {
+      sh = GemvBatchShape{B, C, S};
+      return true;
+    }
+  }
+  return false;
+}
+
+bool gemv_batch_fits(const DevStore &w, int batch) {
+  const int f = kernel_fmt(w.dtype);
+  GemvBatchShape sh;
+  return f >= 0 && chunk_aligned(w, w.cols) &&
+         gemv_batch_shape(f, batch, w.cols / fmt_chunk_elems(f), w.rows, sh);
+}
+
 int fwd_route(const DevStore &w, int batch) {
   if (!chunk_aligned(w, w.cols)) return 3;
   if (g_forward_path) return g_forward_path;
+  // batch 2-8 where x of the batch fits in registers: gemv_loopb_kernel
+  // (4096 x 11008 b4: FP8 14.9 against 19.5 us on the split-x GEMM, NF4 17.1
+  // against 22.2; 11008 x 4096 b4: FP8 16.5 against 22.2, NF4 17.1 against
+  // 24.9)
+  if (batch > 1 && gemv_batch_fits(w, batch)) return 1;
   if (batch <= 2) return 1;
   if (batch > 4) return 2;
-  // batch 3-4: the GEMV re-reads x for every chunk, so its time grows with
+  // other batch 3-4: gemv_kernel re-reads x for every chunk, so its time grows with
   // the batch, while the split-x GEMM's does not; measured crossover between
   // 16.8 M weights (4096^2: GEMV 12.5 against 15.3 us at batch 4) and 45 M
   // (4096 x 11008: 22.1 against 19.4 us FP8, 32.3 against 22.0 NF4)
@@ -2967,13 +3161,68 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// gemv_loopb_kernel launch: R = 16 / (B * C) rows per group (16 sums per
+// group through the butterfly) and a fixed grid walking the row groups.
+// Knob 20 at k >= 2: k waves per CU.  Auto: at B = 2 (no prefetch) 12 waves
+// per CU (for rows of more than 4 waves at most half the group count); from
+// B = 4 on as many blocks as the CUs hold at once (the
+// occupancy query), but at least two row groups per block, so the prefetch
+// has a next group (measured on FP8, FP4 and NF4 at 4096^2, 4096 -> 11008
+// and 11008 -> 4096: it picks the best of 4, 8, 12 and 16 waves per CU).
+template <int F, int C, int R, int B>
+hipError_t launch_loopb(const GemvArgs &a, int batch, int S, hipStream_t s) {
+  const int ngroups = (a.N + R - 1) / R;
+  const int threads = 64 * S;
+  const int k = g_tune[kTuneGemvBatch];
+  int blocks;
+  if (k >= 2) {
+    blocks = k * num_cus() / S;
+  } else if (B == 2) {
+    // rows of more than 4 waves (x of both batch rows: 88 KB per block at
+    // 11008 inputs) at least two groups per block: NF4 11008 -> 4096 13.0
+    // against 15.6 us, FP4 11.2 against 12.8
+    blocks = 12 * num_cus() / S;
+    if (S > 4) blocks = std::min(blocks, (ngroups + 1) / 2);
+  } else {
+    // resident blocks per CU, per waves-per-block count (the kernel's
+    // register count fixes it; queried once per instantiation)
+    static int per_cu[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    if (per_cu[S] == 0) {
+      int nb = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_loopb_kernel<F, C, R, B>, threads, 0) !=
+              hipSuccess ||
+          nb < 1)
+        nb = 1;
+      per_cu[S] = nb;
+    }
+    blocks = std::min(per_cu[S] * num_cus(), (ngroups + 1) / 2);
+  }
+  blocks = std::max(1, std::min(ngroups, blocks));
+  gemv_loopb_kernel<F, C, R, B><<<blocks, threads, 0, s>>>(a, batch);
+  return hipGetLastError();
+}
+
+template <int F>
+hipError_t launch_gemv_batch(const GemvArgs &a, int batch, const GemvBatchShape &sh, hipStream_t s) {
+  const int key = sh.B * 10 + sh.C;
+  if (key == 21) return launch_loopb<F, 1, 8, 2>(a, batch, sh.S, s);
+  if (key == 22) return launch_loopb<F, 2, 4, 2>(a, batch, sh.S, s);
+  if (key == 41) return launch_loopb<F, 1, 4, 4>(a, batch, sh.S, s);
+  if constexpr (FI<F>::kE == 16) {
+    if (key == 42) return launch_loopb<F, 2, 2, 4>(a, batch, sh.S, s);
+    if (key == 81) return launch_loopb<F, 1, 2, 8>(a, batch, sh.S, s);
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
                           int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
                           hipStream_t s) {
   const int route = fwd_route(w, batch);
   const int f = kernel_fmt(w.dtype);
   if (kernel_body(w, f) == nullptr) return hipErrorInvalidValue;
-  if (route == 3 || (route == 1 && batch > 4)) {
+  const bool batched = route == 1 && batch > 1 && gemv_batch_fits(w, batch);
+  if (route == 3 || (route == 1 && batch > 4 && !batched)) {
 #define WH_GEN(D)                                                                        \
   gemv_generic_kernel<D><<<w.rows, 256, 0, s>>>(w, batch, x, bias, bias_len, act, pre, post); \
   return hipGetLastError();
@@ -3080,6 +3329,18 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   return hipGetLastError();
       WH_FMT_SWITCH(f, WH_GV1)
 #undef WH_GV1
+    }
+    if (batched) {
+      GemvBatchShape sh;
+      gemv_batch_shape(f, batch, a.nchunks, a.N, sh);
+      switch (f) {
+      case FE4: return launch_gemv_batch<FE4>(a, batch, sh, s);
+      case FE5: return launch_gemv_batch<FE5>(a, batch, sh, s);
+      case FI8: return launch_gemv_batch<FI8>(a, batch, sh, s);
+      case FF4: return launch_gemv_batch<FF4>(a, batch, sh, s);
+      case FL4P: return launch_gemv_batch<FL4P>(a, batch, sh, s);
+      default: return hipErrorInvalidValue;
+      }
     }
 #define WH_GV(F) return gemv_dispatch<F>(batch, a, s);
     WH_FMT_SWITCH(f, WH_GV)

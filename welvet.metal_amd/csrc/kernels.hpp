@@ -192,7 +192,8 @@ enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kTuneDwBatch = 19, kNumTune = 20
+  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kTuneDwBatch = 19,
+  kTuneGemvBatch = 20, kNumTune = 21
 };
 int set_tuning(int key, int value);
 int tuning(int key);  // the current value (-1 for an unknown key)
