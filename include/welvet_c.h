@@ -344,7 +344,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *     FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4 [1]
  *   11 its weight prefetch depth in k stages: 0 auto (1; 2 on the two-group
  *      workgroups of key 15), 1, 2, or 3 (batch <= 32) [0]
- *   12 its block width: 0 = 256 output columns, 1 = 128 [0]
+ *   12 its block width: 0 auto (128 output columns for at most 8192
+ *      outputs on the 16-row tile and on the one-byte kinds' 32-row tile,
+ *      else 256), 1 = 128, 2 = 256 [0]
  *   13 dW kernel, every one bit-identical to the sequential FMA (the fp32
  *      MFMA accumulates each product with fmaf rounding, in k order): 2 MFMA
  *      with operands staged in LDS (out and in multiples of 128, else 1),

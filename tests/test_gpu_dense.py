@@ -75,7 +75,7 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(gemv_waves=2, gemv_rows=16, cr=3), dict(gemv_waves=1, gemv_rows=1, pair_lut=0),
          dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4), dict(bf3_depth=2),
          dict(bf3_depth=3), dict(bf3_depth=3, gemm_occ=1), dict(bf3_cols=1),
-         dict(bf3_cols=1, gemm_occ=1), dict(dw_mfma=0), dict(bf3_small=0),
+         dict(bf3_cols=1, gemm_occ=1), dict(bf3_cols=2), dict(bf3_cols=2, bf3_small=1), dict(dw_mfma=0), dict(bf3_small=0),
          dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2), dict(bf3_groups=0),
          dict(bf3_depth=1), dict(bf3_groups=0, bf3_depth=2), dict(bf3_groups=1, gemm_occ=2),
          dict(gemv_waves=-2), dict(gemv_waves=-3), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2)]

@@ -2919,8 +2919,18 @@ bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // format
 SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
   if (bk >= 0) {
     const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
-    const int bn = g_tune[kTuneBf3Cols] == 1 ? 128 : 256;
     const int bm = (M <= 16 && g_tune[kTuneBf3Small] != 0) ? 16 : M <= 32 ? 32 : 64;
+    // tile width: 128 output columns where outputs are few (N <= 8192) for
+    // the 16-row tile and for the one-byte kinds' 32-row tile (their
+    // stream-K partial tiles then weigh as much as the weights: 4096^2 FP8
+    // b16 12.9 against 16.3 us, b32 15.2 against 18.1, NF4 b16 14.3 against
+    // 17.2; 11008 -> 4096 FP8 b16 21.4 against 22.9), else 256 (4096 ->
+    // 11008 b8 FP8 19.6 against 20.1; the 4-bit kinds' 32-row tile keeps
+    // the two-group workgroups, which need 256)
+    const int ck = g_tune[kTuneBf3Cols];
+    const bool narrow = ck == 1 || (ck == 0 && N <= 8192 &&
+                                    (bm == 16 || (bm == 32 && bk != BK_NF4 && bk != BK_FP4)));
+    const int bn = narrow ? 128 : 256;
     const int stages = (K + kBK - 1) / kBK;
     // no k split for K <= 2048 (measured at batch 5-16: 1024^2 6.6 against
     // 10.3 us, 2048 -> 4096 9.4 against 14.3; at K = 4096 about even, at
@@ -2984,7 +2994,7 @@ struct GemvBatchShape {
   int B, C, S;
 };
 bool gemv_batch_shape(int f, int batch, int nchunks, int rows, GemvBatchShape &sh) {
-  if (g_tune[kTuneGemvBatch] == 0 || batch < 2 || batch > 8) return false;
+  if (g_tune[kTuneGemvBatch] == 0 || batch < 2 || batch > 8 || nchunks < 1 || rows < 1) return false;
   if (f != FE4 && f != FE5 && f != FI8 && f != FF4 && f != FL4P) return false;
   const int E = fmt_chunk_elems(f);
   const int B = batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
