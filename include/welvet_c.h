@@ -338,7 +338,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *     4, 8, 16 (at most 16 / chunks per lane; FP8, Int8, 4-bit, 8-bit table
  *     and half formats) [0]
  *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
- *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2 and FP4, else 0),
+ *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2 and FP4 and for
+ *     NF4 rows of at most 4096 inputs, 12 for NF4 rows of 5-8 waves, one
+ *     block per group for FP8 rows of 5-8 waves of two chunks, else 0),
  *     -k (k >= 2) = k row groups per block [-1]
  *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
  *     FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4 [1]

@@ -140,12 +140,14 @@ def test_split_x_two_group_workgroups(oracle, dtype):
             pywelvet.set_tuning("bf3_depth", old)
 
 
-@pytest.mark.parametrize("dtype", [16, 26, 14, 15])
+@pytest.mark.parametrize("dtype", [16, 26, 14, 15, 4, 5])
 @pytest.mark.parametrize("cols", [8448, 11008, 8232])
 def test_long_row_gemv(oracle, dtype, cols):
-    """Batch-1 GEMV on rows of three or more waves of two chunks per lane
-    (the 8-rows-per-block default for 4-bit formats): ragged row count, K
-    just past the switch-over and not a multiple of the chunk."""
+    """Batch-1 GEMV on long rows: three or more waves of two chunks per lane
+    (the 8-rows-per-block default for 4-bit formats), NF4 at one chunk per
+    lane over 5-6 waves in the loop, FP8 at two chunks per lane over 5-6
+    waves; ragged row count, K just past the switch-over and not a multiple
+    of the chunk."""
     rng = np.random.default_rng(1400 + dtype + cols)
     W = rng.normal(0, 0.1, (203, cols)).astype(np.float32)
     if dtype == 16:

@@ -553,12 +553,12 @@ __device__ inline double row_reduce(double (&acc)[R], int lane) {
 // wave.  Per-lane fp32 FMA over its C*E products, then an f64 butterfly
 // transpose-reduce over the R rows and an ordered f64 sum over the S slices.
 template <int F, int C, int R>
-__global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(512) gemv_pf_kernel(GemvArgs a) {
   using I = FI<F>;
   using Acc = std::conditional_t<F == FF64, double, float>;
   constexpr int E = I::kE, W = I::kW, NL = I::kTable;
   __shared__ __align__(16) float lut_s[NL];
-  __shared__ double part[4][R];
+  __shared__ double part[8][R];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   TabCopy<F> tab;
   if constexpr (I::kLut) {
@@ -657,14 +657,14 @@ __global__ void __launch_bounds__(256) gemv_pf_kernel(GemvArgs a) {
 // and an ordered f64 sum over the S slices.  The block walks row groups
 // blockIdx.x, blockIdx.x + gridDim.x, ...
 template <int F, int C, int R>
-__global__ void __launch_bounds__(256) gemv_loop_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(512) gemv_loop_kernel(GemvArgs a) {
   using I = FI<F>;
   using Acc = std::conditional_t<F == FF64, double, float>;
   constexpr int E = I::kE, W = I::kW, NL = I::kTable;
   constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
   static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
   __shared__ __align__(16) float lut_s[NL];
-  __shared__ double part[2][4][R];
+  __shared__ double part[2][8][R];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int S = blockDim.x >> 6;
   const int ngroups = (a.N + R - 1) / R;
@@ -3249,7 +3249,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       // chunks per lane cover, 4 rows (measured best: more blocks in flight
       // for the heavier FP8 decode, one wave per block for 4-bit)
       int C = 1, Rauto = 0;
-      bool loop16 = false;
+      int auto_wpc = -1;  // -1: the format's default grid
       switch (g_tune[kTuneCR]) {
       case 1: C = 2; break;
       case 2: C = 4; break;
@@ -3266,14 +3266,25 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         // 9.22-9.30 us with two chunks per lane, one block per group)
         if (f == FL4P && a.nchunks <= 128 &&
             16 * num_cus() / ((a.nchunks + 63) / 64) < (a.N + 3) / 4)
-          C = 1, Rauto = 4, loop16 = true;
+          C = 1, Rauto = 4, auto_wpc = 16;
+        // rows of 5-8 waves of one chunk per lane (8224-16384 inputs of a
+        // 4-bit format): NF4 one chunk per lane, 4 rows per group, the loop
+        // at 12 waves per CU (11008 -> 4096: 9.5 against 10.2 us); FP8 rows
+        // of 5-8 waves of two chunks per lane: two chunks per lane, 8 rows
+        // per block, one block per group (11008 -> 4096: 11.3 against
+        // 13.3-13.9 us with four chunks per lane)
+        {
+          const int s1 = (a.nchunks + 63) / 64, s2 = (a.nchunks + 127) / 128;
+          if (f == FL4P && s1 >= 5 && s1 <= 8) C = 1, Rauto = 4, auto_wpc = 12;
+          if ((f == FE4 || f == FE5) && s1 > 8 && s2 >= 5 && s2 <= 8) C = 2, Rauto = 8, auto_wpc = 0;
+        }
         // 4-bit rows that take three or more waves of two chunks per lane
         // (11008-wide inputs): 8 rows per block (measured at 11008 -> 4096:
         // FP4 8.2 against 9.1 us, NF4 10.2 against 10.6 us with 4)
         if ((f == FL4P || f == FL4 || f == FF4) && C == 2 && a.nchunks > 256) Rauto = 8;
       }
       const int S = (a.nchunks + 64 * C - 1) / (64 * C);
-      if (S <= 4) {
+      if (S <= 8) {
         // rows per block: 8 / C, or the knob's value (else the auto choice)
         // where that (C, R) kernel exists (the formats the sweeps cover)
         int R = 8 / C;
@@ -3288,7 +3299,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         int blocks = ngroups;
         if (wpc < -1) blocks = (ngroups - wpc - 1) / -wpc;  // -k: k row groups per block
         else {
-          if (wpc < 0) wpc = (f == FE4 || f == FE5 || f == FF4 || loop16) ? 16 : 0;
+          if (wpc < 0) wpc = auto_wpc >= 0 ? auto_wpc : (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
           if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
         }
 #define WH_PF(F)                                                                         \
