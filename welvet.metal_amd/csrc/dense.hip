@@ -3195,15 +3195,17 @@ hipError_t launch_loopb(const GemvArgs &a, int batch, int S, hipStream_t s) {
     if (S > 4) blocks = std::min(blocks, (ngroups + 1) / 2);
   } else {
     // resident blocks per CU, per waves-per-block count (the kernel's
-    // register count fixes it; queried once per instantiation)
+    // register count fixes it; queried once per instantiation; concurrent
+    // first calls may both query and store the same value)
     static int per_cu[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     if (per_cu[S] == 0) {
       int nb = 0;
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_loopb_kernel<F, C, R, B>, threads, 0) !=
-              hipSuccess ||
-          nb < 1)
+          hipSuccess) {
+        (void)hipGetLastError();  // a failed query must not read as a failed launch
         nb = 1;
-      per_cu[S] = nb;
+      }
+      per_cu[S] = std::max(nb, 1);
     }
     blocks = std::min(per_cu[S] * num_cus(), (ngroups + 1) / 2);
   }
