@@ -545,6 +545,69 @@ __device__ inline double row_reduce(double (&acc)[R], int lane) {
   return v;
 }
 
+// row_reduce on fp32 values (one 32-bit exchange per value instead of two):
+// the same pairing, so lane l ends with the full sum of row l >> (6 - log2 R)
+// of the wave, added in fp32.
+__device__ inline void swap32f(float &a, float &b) {
+  const u32x2v r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ inline void swap16f(float &a, float &b) {
+  const u32x2v r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ inline float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int R>
+__device__ inline float row_reduce_f32(float (&acc)[R], int lane) {
+  constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
+  static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
+  if constexpr (LR >= 1) {
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) {
+      swap32f(acc[i], acc[i + R / 2]);
+      acc[i] += acc[i + R / 2];
+    }
+  }
+  if constexpr (LR >= 2) {
+#pragma unroll
+    for (int i = 0; i < R / 4; ++i) {
+      swap16f(acc[i], acc[i + R / 4]);
+      acc[i] += acc[i + R / 4];
+    }
+  }
+  if constexpr (LR >= 3) {
+    const bool hi = (lane >> 3) & 1;
+#pragma unroll
+    for (int i = 0; i < R / 8; ++i)
+      acc[i] = (hi ? acc[i + R / 8] : acc[i]) + dppf<0x140>(hi ? acc[i] : acc[i + R / 8]);
+  }
+  if constexpr (LR >= 4) {
+    const bool hi = (lane >> 2) & 1;
+    acc[0] = (hi ? acc[1] : acc[0]) + dppf<0x141>(hi ? acc[0] : acc[1]);
+  }
+  float v = acc[0];
+  if constexpr (LR == 0) {
+    float w = v;
+    swap32f(v, w);
+    v += w;
+  }
+  if constexpr (LR <= 1) {
+    float w = v;
+    swap16f(v, w);
+    v += w;
+  }
+  if constexpr (LR <= 2) v += dppf<0x140>(v);
+  if constexpr (LR <= 3) v += dppf<0x141>(v);
+  v += dppf<0x4E>(v);
+  v += dppf<0xB1>(v);
+  return v;
+}
+
 // Batch-1 GEMV with every load of a lane in flight at once.  A block owns R
 // rows; its S waves split the row into column slices of 64*C chunks (lane i
 // of a wave reads chunk slice*64*C + cc*64 + i of each row: 1 KB contiguous
@@ -774,7 +837,8 @@ __global__ void __launch_bounds__(512) gemv_loop_kernel(GemvArgs a) {
 // all B batch rows in registers, so each weight chunk is loaded and decoded
 // once and feeds B products.  A row group is R rows; its R * B sums (one fp32
 // FMA chain per row and batch row over the lane's C * E products) go through
-// the f64 butterfly as R * B rows, then the ordered f64 sum over the S slices.
+// the butterfly as R * B rows, in fp32, then the ordered f64 sum over the S
+// slices.
 // Batch rows from `batch` to B - 1 read x row batch - 1 and are never stored.
 template <int F, int C, int R, int B>
 __global__ void __launch_bounds__(512) gemv_loopb_kernel(GemvArgs a, int batch) {
@@ -839,7 +903,7 @@ __global__ void __launch_bounds__(512) gemv_loopb_kernel(GemvArgs a, int batch) 
             for (int i = 0; i < W; ++i) w[r][cc][i] &= keep[cc];
       }
     }
-    double acc[V];
+    float acc[V];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float sm[B];
@@ -855,10 +919,12 @@ __global__ void __launch_bounds__(512) gemv_loopb_kernel(GemvArgs a, int batch) 
           for (int b = 0; b < B; ++b) sm[b] = fmaf(v[e], xv[b][cc][e], sm[b]);
       }
 #pragma unroll
-      for (int b = 0; b < B; ++b) acc[r * B + b] = (double)sm[b];
+      for (int b = 0; b < B; ++b) acc[r * B + b] = sm[b];
     }
-    // lane l: the sum of (row, batch row) l >> (6 - LV) over the wave
-    const double v = row_reduce<V>(acc, lane);
+    // lane l: the sum of (row, batch row) l >> (6 - LV) over the wave, in
+    // fp32 (64 lane partials: at most 6 roundings of 2^-24 of the sum of
+    // magnitudes, far inside the 1e-5 bound); the slices add in f64
+    const double v = (double)row_reduce_f32<V>(acc, lane);
     if (S == 1) {
       if ((lane & ((64 >> LV) - 1)) == 0) {
         const int vr = lane >> (6 - LV), row = r0 + vr / B, b = vr % B;
