@@ -716,7 +716,7 @@ __global__ void __launch_bounds__(512) gemv_pf_kernel(GemvArgs a) {
 // 1 KB contiguous per wave per (row, cc)).  Per row group the lane issues all
 // R*C weight loads (non-temporal: the weights are streamed once) before any
 // arithmetic, so one memory latency covers the group.  Per-lane fp32 FMA over
-// its C*E products, then an f64 butterfly transpose-reduce over the R rows
+// its C*E products, then an fp32 butterfly transpose-reduce over the R rows
 // and an ordered f64 sum over the S slices.  The block walks row groups
 // blockIdx.x, blockIdx.x + gridDim.x, ...
 template <int F, int C, int R>
@@ -797,21 +797,21 @@ __global__ void __launch_bounds__(512) gemv_loop_kernel(GemvArgs a) {
             for (int i = 0; i < W; ++i) w[r][cc][i] &= keep[cc];
       }
     }
-    double acc[R];
+    float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      Acc sm[4] = {0, 0, 0, 0};
+      float sm[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int cc = 0; cc < C; ++cc) {
-        Acc v[E];
+        float v[E];
         decode_chunk<F>(w[r][cc], v, lut_s, a.scale, a.minv);
 #pragma unroll
-        for (int e = 0; e < E; ++e) sm[e & 3] = fma(v[e], (Acc)xv[cc][e], sm[e & 3]);
+        for (int e = 0; e < E; ++e) sm[e & 3] = fmaf(v[e], xv[cc][e], sm[e & 3]);
       }
-      acc[r] = ((double)sm[0] + (double)sm[1]) + ((double)sm[2] + (double)sm[3]);
+      acc[r] = (sm[0] + sm[1]) + (sm[2] + sm[3]);
     }
-    // lane l: the sum of row l >> (6 - log2 R) over the wave
-    const double v = row_reduce<R>(acc, lane);
+    // lane l: the sum of row l >> (6 - log2 R) over the wave, in fp32
+    const double v = (double)row_reduce_f32<R>(acc, lane);
     if (S == 1) {
       if ((lane & ((64 >> LR) - 1)) == 0) {
         const int row = r0 + (lane >> (6 - LR));
