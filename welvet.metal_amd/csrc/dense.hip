@@ -3059,14 +3059,21 @@ constexpr int kDxSegRows = 32;
 struct GemvBatchShape {
   int B, C, S;
 };
+// formats gemv_loopb_kernel is built for (fp32 partial sums: not Float64)
+constexpr bool gemv_batch_fmt(int f) {
+  return f == FE4 || f == FE5 || f == FI8 || f == FF4 || f == FL4P || f == FH16 || f == FB16 ||
+         f == FF32 || f == FL8;
+}
 bool gemv_batch_shape(int f, int batch, int nchunks, int rows, GemvBatchShape &sh) {
   if (g_tune[kTuneGemvBatch] == 0 || batch < 2 || batch > 8 || nchunks < 1 || rows < 1) return false;
-  if (f != FE4 && f != FE5 && f != FI8 && f != FF4 && f != FL4P) return false;
+  if (!gemv_batch_fmt(f)) return false;
   const int E = fmt_chunk_elems(f);
   const int B = batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
-  // 8 batch rows only up to 32 M weights (FP8 b8: 4096^2 12.3 against 15.8
-  // us on the split-x GEMM, 4096 x 11008 24.6 against 19.9)
-  if (B == 8 && (int64_t)rows * nchunks * E > ((int64_t)32 << 20)) return false;
+  // 8 batch rows of the split-x GEMM's formats only up to 32 M weights (FP8
+  // b8: 4096^2 12.3 against 15.8 us on that GEMM, 4096 x 11008 24.6 against
+  // 19.9); the others' batch 5-8 GEMM is the fp32 MFMA one, slower still
+  const bool split_x = f == FE4 || f == FE5 || f == FI8 || f == FF4 || f == FL4P;
+  if (B == 8 && split_x && (int64_t)rows * nchunks * E > ((int64_t)32 << 20)) return false;
   for (int C = 1; C <= 2 && B * C * E <= 128; C *= 2) {
     const int S = (nchunks + 64 * C - 1) / (64 * C);
     if (S <= 8) {
@@ -3280,15 +3287,23 @@ hipError_t launch_loopb(const GemvArgs &a, int batch, int S, hipStream_t s) {
   return hipGetLastError();
 }
 
+// One instantiation per (B, C) whose x takes at most 128 registers per lane
+// (B * C * E <= 128), the shapes gemv_batch_shape can choose.
 template <int F>
 hipError_t launch_gemv_batch(const GemvArgs &a, int batch, const GemvBatchShape &sh, hipStream_t s) {
+  constexpr int E = FI<F>::kE;
   const int key = sh.B * 10 + sh.C;
   if (key == 21) return launch_loopb<F, 1, 8, 2>(a, batch, sh.S, s);
-  if (key == 22) return launch_loopb<F, 2, 4, 2>(a, batch, sh.S, s);
-  if (key == 41) return launch_loopb<F, 1, 4, 4>(a, batch, sh.S, s);
-  if constexpr (FI<F>::kE == 16) {
+  if constexpr (4 * E <= 128) {
+    if (key == 22) return launch_loopb<F, 2, 4, 2>(a, batch, sh.S, s);
+    if (key == 41) return launch_loopb<F, 1, 4, 4>(a, batch, sh.S, s);
+  }
+  if constexpr (8 * E <= 128) {
     if (key == 42) return launch_loopb<F, 2, 2, 4>(a, batch, sh.S, s);
     if (key == 81) return launch_loopb<F, 1, 2, 8>(a, batch, sh.S, s);
+  }
+  if constexpr (16 * E <= 128) {
+    if (key == 82) return launch_loopb<F, 2, 1, 8>(a, batch, sh.S, s);
   }
   return hipErrorInvalidValue;
 }
@@ -3428,6 +3443,10 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       case FI8: return launch_gemv_batch<FI8>(a, batch, sh, s);
       case FF4: return launch_gemv_batch<FF4>(a, batch, sh, s);
       case FL4P: return launch_gemv_batch<FL4P>(a, batch, sh, s);
+      case FH16: return launch_gemv_batch<FH16>(a, batch, sh, s);
+      case FB16: return launch_gemv_batch<FB16>(a, batch, sh, s);
+      case FF32: return launch_gemv_batch<FF32>(a, batch, sh, s);
+      case FL8: return launch_gemv_batch<FL8>(a, batch, sh, s);
       default: return hipErrorInvalidValue;
       }
     }
