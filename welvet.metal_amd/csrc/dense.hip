@@ -3052,7 +3052,7 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
 constexpr int kDxSegRows = 32;
 
 // Batch 2-8 on gemv_loopb_kernel: B batch rows in registers (the batch
-// rounded up to 2, 4 or 8), C chunks per lane (1, else 2), S waves per
+// rounded up to 2, 4 or 8), C chunks per lane (1, 2 or 4), S waves per
 // block covering the row (at most 8); false when x of B rows would take more
 // than 128 registers per lane or the row more than 8 waves, or for formats
 // without that kernel.
@@ -3074,7 +3074,8 @@ bool gemv_batch_shape(int f, int batch, int nchunks, int rows, GemvBatchShape &s
   // 19.9); the others' batch 5-8 GEMM is the fp32 MFMA one, slower still
   const bool split_x = f == FE4 || f == FE5 || f == FI8 || f == FF4 || f == FL4P;
   if (B == 8 && split_x && (int64_t)rows * nchunks * E > ((int64_t)32 << 20)) return false;
-  for (int C = 1; C <= 2 && B * C * E <= 128; C *= 2) {
+  // B * C <= 16: at least one row per group of R = 16 / (B * C)
+  for (int C = 1; C <= 4 && B * C <= 16 && B * C * E <= 128; C *= 2) {
     const int S = (nchunks + 64 * C - 1) / (64 * C);
     if (S <= 8) {
       sh = GemvBatchShape{B, C, S};
@@ -3302,8 +3303,12 @@ hipError_t launch_gemv_batch(const GemvArgs &a, int batch, const GemvBatchShape 
     if (key == 42) return launch_loopb<F, 2, 2, 4>(a, batch, sh.S, s);
     if (key == 81) return launch_loopb<F, 1, 2, 8>(a, batch, sh.S, s);
   }
+  if constexpr (8 * E <= 128) {
+    if (key == 24) return launch_loopb<F, 4, 2, 2>(a, batch, sh.S, s);
+  }
   if constexpr (16 * E <= 128) {
     if (key == 82) return launch_loopb<F, 2, 1, 8>(a, batch, sh.S, s);
+    if (key == 44) return launch_loopb<F, 4, 1, 4>(a, batch, sh.S, s);
   }
   return hipErrorInvalidValue;
 }
