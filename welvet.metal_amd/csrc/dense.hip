@@ -3387,7 +3387,15 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
         int blocks = ngroups;
         if (wpc < -1) blocks = (ngroups - wpc - 1) / -wpc;  // -k: k row groups per block
         else {
-          if (wpc < 0) wpc = auto_wpc >= 0 ? auto_wpc : (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
+          if (wpc < 0) {
+            wpc = auto_wpc >= 0 ? auto_wpc : (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
+            // FP8 rows whose 16-wave grid would hold every row group: 12
+            // waves per CU, so the grid walks them (4096^2 config-2 leg:
+            // 5.15 against 5.60 us for one block per group)
+            if ((f == FE4 || f == FE5) && auto_wpc < 0 && 16 * num_cus() / S >= ngroups &&
+                12 * num_cus() / S < ngroups)
+              wpc = 12;
+          }
           if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
         }
 #define WH_PF(F)                                                                         \
