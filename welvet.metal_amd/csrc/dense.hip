@@ -3247,9 +3247,9 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
 
 // gemv_loopb_kernel launch: R = 16 / (B * C) rows per group (16 sums per
 // group through the butterfly) and a fixed grid walking the row groups.
-// Knob 20 at k >= 2: k waves per CU.  Auto: at B = 2 (no prefetch) 12 waves
-// per CU (for rows of more than 4 waves at most half the group count); from
-// B = 4 on as many blocks as the CUs hold at once (the
+// Knob 20 at k >= 2: k waves per CU.  Auto: at B = 2 (no prefetch) 16 waves
+// per CU for rows of at most 4096 inputs, else 12 (past 4 waves at most half
+// the group count); from B = 4 on as many blocks as the CUs hold at once (the
 // occupancy query), but at least two row groups per block, so the prefetch
 // has a next group (measured on FP8, FP4 and NF4 at 4096^2, 4096 -> 11008
 // and 11008 -> 4096: it picks the best of 4, 8, 12 and 16 waves per CU).
@@ -3262,11 +3262,14 @@ hipError_t launch_loopb(const GemvArgs &a, int batch, int S, hipStream_t s) {
   if (k >= 2) {
     blocks = k * num_cus() / S;
   } else if (B == 2) {
-    // rows of more than 4 waves (x of both batch rows: 88 KB per block at
-    // 11008 inputs) at least two groups per block: NF4 11008 -> 4096 13.0
-    // against 15.6 us, FP4 11.2 against 12.8
-    blocks = 12 * num_cus() / S;
-    if (S > 4) blocks = std::min(blocks, (ngroups + 1) / 2);
+    // rows of at most 4096 inputs (x of both batch rows in at most 32 KB per
+    // block): 16 waves per CU (4096 -> 11008 FP8 10.5 against 11.1 us at 12,
+    // 4096^2 Float16 7.4 against 8.4); longer rows 12, and past 4 waves at
+    // least two groups per block (x: 88 KB per block at 11008 inputs; NF4
+    // 11008 -> 4096 13.0 against 15.6 us, FP4 11.2 against 12.8)
+    const bool short_x = a.K <= 4096;
+    blocks = (short_x ? 16 : 12) * num_cus() / S;
+    if (!short_x && S > 4) blocks = std::min(blocks, (ngroups + 1) / 2);
   } else {
     // resident blocks per CU, per waves-per-block count (the kernel's
     // register count fixes it; queried once per instantiation; concurrent
