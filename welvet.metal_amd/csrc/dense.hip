@@ -722,7 +722,7 @@ __global__ void __launch_bounds__(512) gemv_pf_kernel(GemvArgs a) {
 template <int F, int C, int R>
 __global__ void __launch_bounds__(512) gemv_loop_kernel(GemvArgs a) {
   using I = FI<F>;
-  using Acc = std::conditional_t<F == FF64, double, float>;
+  static_assert(F != FF64, "fp32 partial sums: not for Float64 weights");
   constexpr int E = I::kE, W = I::kW, NL = I::kTable;
   constexpr int LR = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4;
   static_assert((1 << LR) == R, "rows per block must be 1, 2, 4, 8 or 16");
@@ -843,6 +843,7 @@ __global__ void __launch_bounds__(512) gemv_loop_kernel(GemvArgs a) {
 template <int F, int C, int R, int B>
 __global__ void __launch_bounds__(512) gemv_loopb_kernel(GemvArgs a, int batch) {
   using I = FI<F>;
+  static_assert(F != FF64, "fp32 partial sums: not for Float64 weights");
   constexpr int E = I::kE, W = I::kW, NL = I::kTable, V = R * B;
   constexpr int LV = V == 2 ? 1 : V == 4 ? 2 : V == 8 ? 3 : 4;
   static_assert((1 << LV) == V, "rows per group times batch rows must be 2, 4, 8 or 16");
