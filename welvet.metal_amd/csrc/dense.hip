@@ -3032,7 +3032,10 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
   // against 82.9, Float64 88 against 106; 4096^2 Int32 b8 23 against 36,
   // ternary 13.2 against 21.8; Float16 equal at b8, 57 against 44 at b16)
   const int rk = g_tune[kTuneBf3Rows];
-  const bool long_k = N <= 8192 && f != FH16 && f != FB16;
+  // at more than 8192 outputs only the 32-bit integer and 2-bit table
+  // formats gain (4096 -> 11008 Int32 b8 / b16 49 / 58 against 83 / 84 us,
+  // ternary 29 / 38.5 against 42 / 41.5; Uint8, Int16, FP6 lose at b16)
+  const bool long_k = f != FH16 && f != FB16 && (N <= 8192 || f == FI32 || f == FU32 || f == FL2);
   if (M <= 16 && K % 4 == 0 && (rk == 2 || (rk == 1 && (K <= 2048 || long_k)))) {
     SkPlan p;
     p.rows = true;
