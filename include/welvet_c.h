@@ -361,8 +361,10 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      (epilogue in the kernel, no reduction launch; the split-x GEMM for
  *      its formats, the fp32 MFMA for the others): 0 off, 1 for a
  *      reduction length <= 2048 (and, for the fp32-MFMA forward outside
- *      Float16 / BFloat16, any length at <= 8192 outputs, or at any width
- *      for 32-bit integer and 2-bit table weights), 2 always [1]
+ *      Float16 / BFloat16, any length at <= 8192 outputs, for 16-bit
+ *      integers at lengths <= 4096 or batch <= 8, and at any width for
+ *      32- and 64-bit integer, 1- to 3-bit table and Complex128 weights),
+ *      2 always [1]
  *   17 volume training steps: a piecewise activation's derivative (ReLU,
  *      ReLU2, LeakyReLU) applied in the epilogue of the layer above's
  *      no-split dX instead of a launch of its own [1]

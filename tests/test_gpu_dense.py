@@ -223,11 +223,12 @@ def test_small_batch_no_split_gemm(oracle, dtype):
             pywelvet.set_tuning("bf3_rows", old)
 
 
-@pytest.mark.parametrize("dtype", [7, 11, 17, 19])
+@pytest.mark.parametrize("dtype", [7, 11, 17, 19, 20, 32, 6, 25])
 def test_no_split_gemm_wide_outputs(oracle, dtype):
     """Batch 9-16 forwards of the formats that take the no-split fp32-MFMA
-    GEMM past K = 2048 also at more than 8192 outputs (32-bit integers, 2-bit
-    tables): 8448 outputs, K = 2112 (ragged last stage), batch 12 and 16."""
+    GEMM past K = 2048 also at more than 8192 outputs (32- and 64-bit
+    integers, 1- to 3-bit tables, Complex128): 8448 outputs, K = 2112
+    (ragged last stage), batch 12 and 16."""
     rng = np.random.default_rng(1800 + dtype)
     W = rng.normal(0, 2112 ** -0.5, (8448, 2112)).astype(np.float32)
     for batch in (12, 16):

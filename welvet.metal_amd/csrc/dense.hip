@@ -3027,15 +3027,21 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     return p;
   }
   // batch <= 16 without a k split (gemm_regr_kernel): K <= 2048 as for the
-  // split-x 16-row GEMM, and any K for at most 8192 outputs outside the half
-  // formats (11008 -> 4096 b8: Uint8 29.9 against 44.5 us, Float32 62.4
-  // against 82.9, Float64 88 against 106; 4096^2 Int32 b8 23 against 36,
-  // ternary 13.2 against 21.8; Float16 equal at b8, 57 against 44 at b16)
+  // split-x 16-row GEMM, and any K (per format, measured at 4096^2, 4096 <->
+  // 11008, batch 8 and 16) for at most 8192 outputs outside the half formats
+  // (11008 -> 4096 b8: Uint8 29.9 against 44.5 us, Float32 62.4 against
+  // 82.9, Int64 72.6 against 114; Float16 57 against 44 at b16), the 16-bit
+  // integers there only at K <= 4096 or batch <= 8 (11008 -> 4096 b16 Uint16
+  // 57.2 against 46.7), and at more outputs for the formats that gain there
+  // too (4096 -> 11008 b8 / b16: Int32 49 / 58 against 83 / 84, the 1- to
+  // 3-bit tables 29-30 / 38-40 against 42 / 42, Int64 82 / 86 against 110 /
+  // 112, Complex128 167 / 177 against 190 / 183; Uint8, Uint16, FP6, Int5
+  // and Complex64 lose at b16)
   const int rk = g_tune[kTuneBf3Rows];
-  // at more than 8192 outputs only the 32-bit integer and 2-bit table
-  // formats gain (4096 -> 11008 Int32 b8 / b16 49 / 58 against 83 / 84 us,
-  // ternary 29 / 38.5 against 42 / 41.5; Uint8, Int16, FP6 lose at b16)
-  const bool long_k = f != FH16 && f != FB16 && (N <= 8192 || f == FI32 || f == FU32 || f == FL2);
+  const bool half = f == FH16 || f == FB16, int16 = f == FI16 || f == FU16;
+  const bool wide_ok = f == FI32 || f == FU32 || f == FI64 || f == FU64 || f == FL1 || f == FL2 ||
+                       f == FL3 || f == FC128;
+  const bool long_k = !half && (N <= 8192 ? (!int16 || K <= 4096 || M <= 8) : wide_ok);
   if (M <= 16 && K % 4 == 0 && (rk == 2 || (rk == 1 && (K <= 2048 || long_k)))) {
     SkPlan p;
     p.rows = true;
