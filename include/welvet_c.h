@@ -374,10 +374,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      chain, up to 16 layers per launch (layers whose sizes are multiples
  *      of 128), 0 = each with its layer's backward [1]
  *   20 batch 2-8 forward as a GEMV that keeps x of every batch row in
- *      registers (FP8 E4M3 / E5M2, Int8, FP4, NF4, Float32, Float16,
- *      BFloat16 and the 8-bit table formats; rows of at most 8 waves, x of
- *      at most 128 registers per lane; the split-x formats' batch 5-8 up to
- *      32 M weights):
+ *      registers (every format but Float64 and the complex ones; rows of at
+ *      most 8 waves, x of at most 128 registers per lane; the split-x
+ *      formats' batch 5-8 up to 32 M weights):
  *      0 off, 1 on with an automatic grid, k >= 2 on with k waves per CU
  *      walking the row groups [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);

@@ -278,7 +278,7 @@ def test_loop_gemv_ragged_rows(oracle, dtype):
             pywelvet.set_tuning(k, v)
 
 
-@pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26, 1, 2, 3, 13])
+@pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26, 1, 2, 3, 13, 8, 12, 7, 6, 17, 20, 32, 30, 27])
 def test_batched_gemv(oracle, dtype):
     """Batch 2-8 through the GEMV that holds x of every batch row in
     registers: batches that fill and that pad its 2 / 4 / 8 register rows,

@@ -3076,7 +3076,8 @@ struct GemvBatchShape {
 // formats gemv_loopb_kernel is built for (fp32 partial sums: not Float64)
 constexpr bool gemv_batch_fmt(int f) {
   return f == FE4 || f == FE5 || f == FI8 || f == FF4 || f == FL4P || f == FH16 || f == FB16 ||
-         f == FF32 || f == FL8;
+         f == FF32 || f == FL8 || f == FI16 || f == FU16 || f == FI32 || f == FU32 || f == FI64 ||
+         f == FU64 || f == FL1 || f == FL2 || f == FL3 || f == FL5 || f == FL6;
 }
 bool gemv_batch_shape(int f, int batch, int nchunks, int rows, GemvBatchShape &sh) {
   if (g_tune[kTuneGemvBatch] == 0 || batch < 2 || batch > 8 || nchunks < 1 || rows < 1) return false;
@@ -3477,6 +3478,17 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
       case FB16: return launch_gemv_batch<FB16>(a, batch, sh, s);
       case FF32: return launch_gemv_batch<FF32>(a, batch, sh, s);
       case FL8: return launch_gemv_batch<FL8>(a, batch, sh, s);
+      case FI16: return launch_gemv_batch<FI16>(a, batch, sh, s);
+      case FU16: return launch_gemv_batch<FU16>(a, batch, sh, s);
+      case FI32: return launch_gemv_batch<FI32>(a, batch, sh, s);
+      case FU32: return launch_gemv_batch<FU32>(a, batch, sh, s);
+      case FI64: return launch_gemv_batch<FI64>(a, batch, sh, s);
+      case FU64: return launch_gemv_batch<FU64>(a, batch, sh, s);
+      case FL1: return launch_gemv_batch<FL1>(a, batch, sh, s);
+      case FL2: return launch_gemv_batch<FL2>(a, batch, sh, s);
+      case FL3: return launch_gemv_batch<FL3>(a, batch, sh, s);
+      case FL5: return launch_gemv_batch<FL5>(a, batch, sh, s);
+      case FL6: return launch_gemv_batch<FL6>(a, batch, sh, s);
       default: return hipErrorInvalidValue;
       }
     }
