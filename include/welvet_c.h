@@ -363,7 +363,8 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      reduction length <= 2048 (and, for the fp32-MFMA forward outside
  *      Float16 / BFloat16, any length at <= 8192 outputs, for 16-bit
  *      integers at lengths <= 4096 or batch <= 8, and at any width for
- *      32- and 64-bit integer, 1- to 3-bit table and Complex128 weights),
+ *      32- and 64-bit integer, 1- to 3-bit table and Complex128 weights;
+ *      the dX up to 4096 rows and 8192 columns outside FP8 and Int8),
  *      2 always [1]
  *   17 volume training steps: a piecewise activation's derivative (ReLU,
  *      ReLU2, LeakyReLU) applied in the epilogue of the layer above's

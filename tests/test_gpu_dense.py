@@ -192,13 +192,14 @@ def test_small_batch_no_split_gemm(oracle, dtype):
     fp32-MFMA formats, the 16-row split-x GEMM for the others): ragged N (70,
     300 and 1000 rows), K of 2.5 stages (320), at the K <= 2048 bound, past
     it (4160: the fp32-MFMA formats' rule for at most 8192 outputs), a
-    1024^2 layer at batch 16, bias + activation, and the same cases with the
-    no-split route off and forced.  W ~ N(0, 1/K) keeps pre of order 1,
+    1024^2 layer at batch 16, a dX over 3000 rows (past 2048: the rule for
+    formats without a transposed copy), bias + activation, and the same
+    cases with the no-split route off and forced.  W ~ N(0, 1/K) keeps pre of order 1,
     where a saturating activation's output is compared at the scale its
     input has."""
     rng = np.random.default_rng(1700 + dtype)
     cases = [(70, 320, 5, -1), (1000, 2048, 16, 1), (1024, 1024, 16, 3), (70, 320, 13, 0),
-             (300, 4160, 12, -1)]
+             (300, 4160, 12, -1), (3000, 512, 12, -1)]
     for knob in (1, 0, 2):
         old = pywelvet.set_tuning("bf3_rows", knob)
         try:
