@@ -279,6 +279,21 @@ def test_loop_gemv_ragged_rows(oracle, dtype):
             pywelvet.set_tuning(k, v)
 
 
+@pytest.mark.parametrize("dtype", [4, 26, 2, 7])
+def test_batched_gemv_bias_act(oracle, dtype):
+    """The batch 2-8 GEMV's epilogue: one bias per output row for every batch
+    row (shorter than the outputs: rows past it take none), each activation,
+    on one-wave and multi-wave rows with a partial last group."""
+    rng = np.random.default_rng(53 + dtype)
+    for out, inn in ((203, 4096), (37, 1024)):
+        W = rng.normal(0, inn ** -0.5, (out, inn)).astype(np.float32)
+        bias = rng.normal(0, 0.5, out - 5)
+        for act in (0, 1, 2, 3):
+            for batch in (2, 3, 6):
+                x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+                check_forward(oracle, dtype, W, x, act=act, bias=bias)
+
+
 @pytest.mark.parametrize("dtype", [4, 5, 9, 16, 26, 1, 2, 3, 13, 8, 12, 7, 6, 17, 20, 32, 30, 27])
 def test_batched_gemv(oracle, dtype):
     """Batch 2-8 through the GEMV that holds x of every batch row in
