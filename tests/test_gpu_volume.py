@@ -240,12 +240,13 @@ def test_device_forward_writes_the_callers_buffer(oracle):
 
 
 @pytest.mark.parametrize("dtype", [1, 4, 26])
-@pytest.mark.parametrize("batch", [5, 16])
+@pytest.mark.parametrize("batch", [5, 16, 40])
 def test_train_derivative_in_dx_epilogue(oracle, dtype, batch):
     """The piecewise activation derivatives (ReLU, ReLU2, LeakyReLU hidden
     layers) applied in the layer above's dX epilogue give the same losses and
     stored bytes, bit for bit, as the separate derivative launch, and the
-    steps agree with the oracle."""
+    steps agree with the oracle.  Batch 40 folds it into the reduction of the
+    stream-K dX GEMMs, the smaller batches into the no-split dX kernel."""
     from parity import assert_bit_equal
 
     rng = np.random.default_rng(2300 + 3 * dtype + batch)

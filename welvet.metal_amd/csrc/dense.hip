@@ -2373,10 +2373,14 @@ done:
 // Sum of a tile's stream-K partials in workgroup order (f64).  Grid: x =
 // tile, y = 1024-element slice of the tile; each thread adds four adjacent
 // outputs with float4 loads.  The forward applies bias + activation, dX
-// stores fl32 of the sum.
+// stores fl32 of the sum, times act'(next_pre) when next_pre is given (in
+// a volume training step the pre of the layer below, act its piecewise
+// activation: the derivative act_deriv_kernel would apply, the same
+// expression as gemm_regt_kernel's NEXT epilogue).
 template <bool FWD>
 __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double *bias, int bias_len,
-                                                        int act, float *out, float *post) {
+                                                        int act, float *out, float *post,
+                                                        const float *next_pre) {
   const int t = blockIdx.x;
   const int b0 = (int)((int64_t)t * a.nst / a.per_block);
   const int b1 = (int)(((int64_t)(t + 1) * a.nst - 1) / a.per_block);
@@ -2411,6 +2415,7 @@ __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double
   // as one 16-byte write per output array where the row allows it
   float pv[4], qv[4];
   const int nv = min(4, a.N - n);
+  const int64_t idx = (int64_t)m * a.N + n;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (a.post != 1.0f) sum[i] *= (double)a.post;
@@ -2418,10 +2423,11 @@ __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double
     if constexpr (FWD) {
       if (bias != nullptr && n + i < bias_len) p = (float)((double)p + bias[n + i]);
       qv[i] = i < nv ? act_value(p, act) : 0.0f;
+    } else {
+      if (next_pre != nullptr && i < nv) p = p * act_prime_piecewise(next_pre[idx + i], act);
     }
     pv[i] = p;
   }
-  const int64_t idx = (int64_t)m * a.N + n;
   if (nv == 4 && (a.N & 3) == 0) {
     *(float4 *)(out + idx) = make_float4(pv[0], pv[1], pv[2], pv[3]);
     if constexpr (FWD) *(float4 *)(post + idx) = make_float4(qv[0], qv[1], qv[2], qv[3]);
@@ -3532,7 +3538,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  sk_reduce_kernel<true><<<sk_reduce_grid(p), 256, 0, s>>>(a, bias, bias_len, act, pre, post);
+  sk_reduce_kernel<true><<<sk_reduce_grid(p), 256, 0, s>>>(a, bias, bias_len, act, pre, post, nullptr);
   return hipGetLastError();
 }
 
@@ -3622,8 +3628,15 @@ hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The dX kernels whose epilogue applies the lower layer's derivative: the
+// no-split gemm_regt_kernel and the reduction of the stream-K GEMMs
+// (sk_reduce_kernel); not the transposed no-split bf3r epilogue.
 bool backward_dx_applies_next(const DevStore &w, int batch, int next_act) {
-  return g_tune[kTuneFoldDeriv] != 0 && act_piecewise(next_act) && dx_rows(w, batch);
+  if (g_tune[kTuneFoldDeriv] == 0 || !act_piecewise(next_act)) return false;
+  if (dx_rows(w, batch)) return true;
+  if (dx_route(w, batch) != 2) return false;
+  const int bk = dx_bf3_kind(w, batch);
+  return bk < 0 || !plan_fwd_gemm(kernel_fmt(w.dtype), bk, batch, w.rows, w.cols).rows;
 }
 
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
@@ -3681,7 +3694,8 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     } else {
       e = launch_bf3(p, bk, a, s);
       if (e != hipSuccess) return e;
-      sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
+      sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, chain.dx_next_act, dX, nullptr,
+                                                                chain.dx_next_pre);
     }
   } else if (dx_rows(w, batch)) {
     const int st = dx_rows_stage(f);
@@ -3707,7 +3721,8 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
 #undef WH_DXM
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, -1, dX, nullptr);
+    sk_reduce_kernel<false><<<sk_reduce_grid(p), 256, 0, s>>>(a, nullptr, 0, chain.dx_next_act, dX, nullptr,
+                                                              chain.dx_next_pre);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
