@@ -3744,9 +3744,46 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   return hipGetLastError();
 }
 
+// transpose_u8_kernel for rows a multiple of 64 and cols of 256 (every tile
+// whole): a 64 x 256-byte tile goes through LDS as 4-byte words; each thread
+// reads a 16 x 4 byte block (one word column of 16 input rows), transposes
+// its four 4 x 4 blocks in registers and writes four 16-byte pieces of four
+// output rows; the 4 threads of one word column write 64 contiguous bytes of
+// each of its output rows.
+__global__ void __launch_bounds__(256) transpose_u8_tile_kernel(const uint8_t *__restrict__ in, int rows,
+                                                                int cols, uint8_t *__restrict__ out) {
+  __shared__ uint32_t t[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 256, tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int lr = k * 16 + (tid >> 4), lw = (tid & 15) * 4;  // 16 pieces of 16 bytes per row
+    const uint4 v = *(const uint4 *)(in + (int64_t)(r0 + lr) * cols + c0 + lw * 4);
+    t[lr][lw] = v.x;
+    t[lr][lw + 1] = v.y;
+    t[lr][lw + 2] = v.z;
+    t[lr][lw + 3] = v.w;
+  }
+  __syncthreads();
+  const int rb = tid & 3, a = tid >> 2;  // input rows 16rb..16rb+15, input columns 4a..4a+3
+  uint32_t w[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) w[k] = t[16 * rb + k][a];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = ((w[4 * q] >> (8 * j)) & 0xffu) | (((w[4 * q + 1] >> (8 * j)) & 0xffu) << 8) |
+             (((w[4 * q + 2] >> (8 * j)) & 0xffu) << 16) | (((w[4 * q + 3] >> (8 * j)) & 0xffu) << 24);
+    *(uint4 *)(out + (int64_t)(c0 + 4 * a + j) * rows + r0 + 16 * rb) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *out, hipStream_t s) {
-  const dim3 g((cols + 63) / 64, (rows + 63) / 64);
-  transpose_u8_kernel<<<g, 256, 0, s>>>(in, rows, cols, out);
+  if (rows % 64 == 0 && cols % 256 == 0)
+    transpose_u8_tile_kernel<<<dim3(cols / 256, rows / 64), 256, 0, s>>>(in, rows, cols, out);
+  else
+    transpose_u8_kernel<<<dim3((cols + 63) / 64, (rows + 63) / 64), 256, 0, s>>>(in, rows, cols, out);
   return hipGetLastError();
 }
 
