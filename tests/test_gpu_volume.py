@@ -281,6 +281,32 @@ def test_train_derivative_in_dx_epilogue(oracle, dtype, batch):
         assert_bit_equal(runs[1][1][co], runs[0][1][co], f"store {co}")
 
 
+@pytest.mark.parametrize("dtype", [4, 5, 9])
+def test_train_transposed_codes_whole_tiles(oracle, dtype):
+    """A training step whose second layer (512 inputs, a multiple of 256)
+    refreshes its transposed codes through whole 64 x 256-byte tiles and
+    takes dX through them at batch 32: outputs, losses and stored bytes
+    follow the oracle over three steps."""
+    rng = np.random.default_rng(2500 + dtype)
+    widths = [256, 512, 256]
+    acts = [0, -1]
+    spec = {(0, 0, l, 0): (rng.normal(0, 0.05, (widths[l + 1], widths[l])).astype(np.float32),
+                           acts[l], dtype, None) for l in range(2)}
+    x = rng.normal(0, 1, (32, widths[0])).astype(np.float32)
+    t = rng.normal(0, 1, (32, widths[-1])).astype(np.float32)
+    G, V = build(oracle, (1, 1, 2, 1), 32, spec)
+    with G:
+        for step in range(3):
+            loss, y = G.train_step(x, t, 1e-2)
+            code, _, rloss, ry = V.train_step(x, t, 1e-2)
+            assert code == 0
+            assert rel_err(y, ry) <= 4 * 1e-5, (step, rel_err(y, ry))
+            assert abs(loss - rloss) <= 1e-4 * max(1.0, abs(rloss)), (step, loss, rloss)
+            _check_weights(G, V, spec, f"whole-tile step {step}")
+            for co in spec:
+                V.cells[co]["raw"] = G.native(co)[0].copy()
+
+
 @pytest.mark.parametrize("dtypes,widths,xs,lr", [
     ([1, 1, 4, 4, 26, 9], [128, 256, 128, 256, 128, 128, 128], 1.0, 1e-2),
     ([5, 5, 5, 0, 16, 16], [64, 128, 128, 256, 128, 96, 48], 0.05, 1e-3)],
