@@ -121,3 +121,24 @@ def test_sgd_rejects_nonfinite(oracle):
     with pywelvet.Session(w, batch=1, dtype=1) as s:
         assert s.sgd(g, 0.1, status=True).code == 2  # training.mm:122-124
         assert s.sgd(np.zeros_like(w), 1e300, status=True).code == 2  # training.mm:75-78
+
+
+@pytest.mark.parametrize("dtype", [9, 4], ids=["int8", "e4m3"])
+def test_sgd_reencode_at_config4_size(dtype, oracle):
+    """WeightStore::apply_sgd on config 4's 8192 x 2048 store (16.8 M codes:
+    the 16-codes-per-thread kernel) with a host gradient: every native byte
+    equal to the oracle's re-encode, and a fair share of the codes moved."""
+    rng = np.random.default_rng(2100 + dtype)
+    shape = (8192, 2048)
+    w = (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02 if dtype == 9 else 1.0))
+    g = rng.standard_normal(shape, dtype=np.float32)
+    lr = 2e-3 if dtype == 9 else 2e-2
+    with pywelvet.Session(w, batch=1, dtype=dtype) as s:
+        before, _ = s.native()
+        s.sgd(g, lr)
+        native, _ = s.native()
+    raw, scale = oracle.pack(dtype, w)
+    assert_bit_equal(before, raw, "packed")
+    assert oracle.native_sgd(dtype, raw, scale, w.size, g, lr) == 0
+    assert_bit_equal(native, raw, f"{DTYPE_NAMES[dtype]} 8192x2048 sgd native")
+    assert np.count_nonzero(native != before) > w.size // 20

@@ -215,3 +215,93 @@ def test_c5_grid_step_every_dtype(oracle, dtype):
                 continue
             same = (a == b) | (np.isnan(a) & np.isnan(b))
             assert 1.0 - same.mean() <= 1e-2, (co, 1.0 - same.mean())
+
+
+def _dyadic_c4(rng, dtype):
+    """Config 4's shapes with values on small dyadic grids, so that every
+    forward, MSE-gradient and dX value is exact in f32 (partial sums stay far
+    inside 24 bits), on the GPU and in the oracle alike: the dW (sequential
+    FMA) and the SGD re-encode then see identical inputs, and the stores after
+    the step can be compared bit for bit.  One weight of each matrix is
+    127/64, so the Int8 scale is exactly 2^-6 (E4M3 stores it as 2)."""
+    def mat(shape):
+        W = rng.integers(-1, 2, shape).astype(np.float32) * np.float32(2.0 ** -6)
+        W[0, 0] = np.float32(127 * 2.0 ** -6)
+        return W
+    x = rng.integers(-1, 2, (256, 2048)).astype(np.float32)
+    t = rng.integers(-256, 257, (256, 2048)).astype(np.float32) * np.float32(2.0 ** -12)
+    return mat((8192, 2048)), mat((2048, 8192)), x, t
+
+
+@pytest.mark.parametrize("sgd_batch", [1, 0], ids=["batched-sgd", "per-store-sgd"])
+@pytest.mark.parametrize("dtype", [9, 4], ids=["int8", "e4m3"])
+def test_c4_exact_step_stores_bit_exact(oracle, dtype, sgd_batch):
+    """One config-4 training step (2048 -> 8192 -> 2048, ReLU then Linear,
+    batch 256) on exact dyadic data: the output equals the oracle's bit for
+    bit, and after SGD (lr 256: the MSE gradient carries 1/n = 2^-19, so this
+    moves a fair share of the codes) both 16.8 M-code stores equal the
+    oracle's bit for bit — through the two-store SGD launch and through one
+    launch per store."""
+    from parity import assert_bit_equal
+
+    rng = np.random.default_rng(SEED + 30 + dtype)
+    W0, W1, x, t = _dyadic_c4(rng, dtype)
+    lr = 256.0
+    coords = [(0, 0, 0, 0), (0, 0, 1, 0)]
+    old = pywelvet.set_tuning("sgd_batch", sgd_batch)
+    try:
+        G = pywelvet.Grid(1, 1, 2, 1, 256)
+        V = Volume(oracle, 1, 1, 2, 1, 256)
+        for co, W, act in zip(coords, (W0, W1), (0, -1)):
+            G.bind_dense(co, W, act=act, dtype=dtype)
+            V.bind_dense(co, W, act=act, dtype=dtype)
+        with G:
+            before = [G.native(co)[0].copy() for co in coords]
+            loss, y = G.train_step(x, t, lr)
+            code, msg, rloss, ry = V.train_step(x, t, lr)
+            assert code == 0, msg
+            assert_bit_equal(y, ry, "c4 exact forward")
+            assert abs(loss - rloss) <= 1e-12 * abs(rloss), (loss, rloss)
+            for i, co in enumerate(coords):
+                got = G.native(co)[0]
+                assert_bit_equal(got, V.cells[co]["raw"], f"c4 exact store {co}")
+                moved = np.count_nonzero(got != before[i])
+                say(f"c4 exact {DTYPE_NAMES[dtype]} sgd_batch={sgd_batch} {co}: {moved} codes moved")
+                assert moved > got.size // 1000
+    finally:
+        pywelvet.set_tuning("sgd_batch", old)
+
+
+@pytest.mark.parametrize("dtype", [9, 4], ids=["int8", "e4m3"])
+def test_c4_ten_steps_without_resync(oracle, dtype):
+    """Config 4 as specified: ten training steps at lr 1e-3, the GPU and the
+    oracle each continuing from their own stores (training.cpp:161-184).  At
+    every step the output and the loss stay within the two layers' budget
+    and the stored codes within the one-step bound."""
+    rng = np.random.default_rng(SEED + 3 + dtype)
+    widths = [2048, 8192, 2048]
+    batch, lr = 256, 1e-3
+    G = pywelvet.Grid(1, 1, 2, 1, batch)
+    V = Volume(oracle, 1, 1, 2, 1, batch)
+    coords = [(0, 0, 0, 0), (0, 0, 1, 0)]
+    for l, co in enumerate(coords):
+        W = normal(rng, (widths[l + 1], widths[l]), 0.02)
+        act = 0 if l == 0 else -1
+        G.bind_dense(co, W, act=act, dtype=dtype)
+        V.bind_dense(co, W, act=act, dtype=dtype)
+    x = normal(rng, (batch, widths[0]), 1.0)
+    t = normal(rng, (batch, widths[-1]), 1.0)
+    budget = tol_for_k(2048) + tol_for_k(8192)
+    losses = []
+    with G:
+        for step in range(10):
+            loss, y = G.train_step(x, t, lr)
+            code, msg, rloss, ry = V.train_step(x, t, lr)
+            assert code == 0, msg
+            e = rel_err(y, ry)
+            say(f"c4 {DTYPE_NAMES[dtype]} 10-step run, step {step}: loss {loss!r} vs {rloss!r}, y rel err {e:.2e}")
+            assert e <= budget, (step, e)
+            assert abs(loss - rloss) <= budget * abs(rloss), (step, loss, rloss)
+            compare_weights(G, V, coords, f"c4 10-step run, step {step}")
+            losses.append(rloss)
+    say(f"c4 {DTYPE_NAMES[dtype]} oracle losses: {losses}")

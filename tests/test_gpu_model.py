@@ -168,3 +168,36 @@ def test_grid_session(oracle):
         assert (st.code, st.message.decode()) == (1, "grid synchronization is configured per cell at mount")
         st, _ = m.call("backward", wire.tensor(x) + wire.tensor(t))
         assert (st.code, st.message.decode()) == (1, "segment backward expects Stack or Parallel")
+
+
+def test_grid_session_trains_at_two_batches(oracle):
+    """A grid session trained at batch 2 and then at batch 6: the second step
+    needs every cell's [batch][out] gradient buffer at the larger batch (the
+    step's dX writes the cell below's buffer, the derivative is applied in
+    place).  Each step's loss and stores agree with the oracle's volume at
+    that batch started from the session's own stores."""
+    rng = np.random.default_rng(902)
+    dims = (1, 1, 1, 3)
+    cells = {(0, 0, 0, 0): dict(W=rng.normal(0, 0.1, (128, 64)).astype(np.float32), act=0, dtype=9),
+             (0, 0, 0, 1): dict(W=rng.normal(0, 0.1, (256, 128)).astype(np.float32), act=6, dtype=1),
+             (0, 0, 0, 2): dict(W=rng.normal(0, 0.1, (128, 256)).astype(np.float32), act=-1, dtype=4)}
+    desc = model_desc.grid(oracle, dims, cells)
+    order = [co for co in wire.hops(dims) if co in cells]
+    with pywelvet.Model(desc) as m:
+        for batch in (2, 6, 3):
+            before = wire.read_nws1(m.export()[1])[0]
+            V = Volume(oracle, *dims, batch)
+            for co, c in cells.items():
+                V.bind_dense(co, c["W"], act=c["act"], dtype=c["dtype"])
+            for got, co in zip(before, order):
+                c = V.cells[co]
+                c["raw"] = (got["f32"].view(np.uint8) if c["dtype"] == 1 else got["raw"]).copy()
+            x = rng.normal(0, 1, (batch, 64)).astype(np.float32)
+            t = rng.normal(0, 1, (batch, 128)).astype(np.float32)
+            st, loss = m.train_mse(1, 1e-2, wire.tensor(x) + wire.tensor(t))
+            assert st.code == 0, st.message
+            code, _, oloss, _ = V.train_step(x, t, 1e-2)
+            assert code == 0 and abs(loss - oloss) <= 3e-5 * oloss, (batch, loss, oloss)
+            for got, co in zip(wire.read_nws1(m.export()[1])[0], order):
+                c = V.cells[co]
+                _check_store(got, c["raw"], c["scale"], c["dtype"], f"batch {batch} {co}")

@@ -355,3 +355,42 @@ def test_train_batched_sgd_and_dw_match_per_cell(oracle, dtypes, widths, xs, lr)
         assert runs[knobs][0] == runs[(1, 1)][0], (knobs, runs[knobs][0], runs[(1, 1)][0])
         for co in spec:
             assert_bit_equal(runs[knobs][1][co], runs[(1, 1)][1][co], f"store {co} knobs {knobs}")
+
+
+@pytest.mark.parametrize("dtype", [9, 13, 14], ids=["int8", "uint8", "int4"])
+def test_batched_sgd_bad_last_store_updates_the_earlier_ones(oracle, dtype):
+    """One SGD launch for two stores of one dtype where only the second
+    store's dW is non-finite: the first store (1 M weights, many blocks) is
+    updated in full, bit for bit as with a launch per store, and the step
+    reports the reference's code.  Layer 0 has weights near 1e25, so the
+    top layer's dW = dpre ⊗ h overflows f32 while layer 0's dW stays finite."""
+    from parity import assert_bit_equal
+
+    rng = np.random.default_rng(2600 + dtype)
+    W0 = (rng.normal(0, 1, (1024, 1024)) * 1e25).astype(np.float32)
+    W1 = rng.normal(0, 0.05, (64, 1024)).astype(np.float32)
+    x = rng.normal(0, 1, (4, 1024)).astype(np.float32)
+    t = rng.normal(0, 1, (4, 64)).astype(np.float32)
+    spec = {(0, 0, 0, 0): (W0, -1, dtype, None), (0, 0, 0, 1): (W1, -1, dtype, None)}
+    runs = {}
+    for knob in (1, 0):
+        old = pywelvet.set_tuning("sgd_batch", knob)
+        try:
+            G, V = build(oracle, (1, 1, 1, 2), 4, spec)
+            with G:
+                before = [G.native(co)[0].copy() for co in spec]
+                st, loss, _ = G.train_step(x, t, 1.0, status=True)
+                after = [G.native(co)[0].copy() for co in spec]
+            runs[knob] = (st.code, st.message.decode(), before, after)
+        finally:
+            pywelvet.set_tuning("sgd_batch", old)
+    code, msg, before, after = runs[1]
+    assert (code, msg) == (1, "weights: nonfinite gradient")
+    assert runs[0][:2] == (code, msg)
+    # the bad store is untouched, the good one moved, both as per-store launches
+    assert_bit_equal(after[1], before[1], "bad store")
+    assert (after[0] != before[0]).any()
+    for i in range(2):
+        assert_bit_equal(after[i], runs[0][3][i], f"store {i}")
+    ocode, _, _, _ = V.train_step(x, t, 1.0)
+    assert ocode == 1

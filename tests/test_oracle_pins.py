@@ -182,6 +182,11 @@ def test_activation_special_points(oracle):
     assert oracle.act_prime(0.0, ACT["relu"]) == 0.0      # v > 0 ? 1 : 0
     assert oracle.act_prime(0.0, ACT["relu2"]) == 0.0
     assert oracle.act_prime(-1.0, ACT["leakyrelu"]) == np.float32(0.01)
+    # v > 0 ? 1 : 0.01f (ops_common.metal:135-136): the slope at exactly 0 is
+    # the negative side's, the f32 constant
+    assert oracle.act_prime(0.0, ACT["leakyrelu"]) == np.float32(0.01)
+    assert oracle.act_prime(-0.0, ACT["leakyrelu"]) == np.float32(0.01)
+    assert oracle.act_prime(2.0 ** -140, ACT["leakyrelu"]) == 1.0
     assert oracle.act_prime(0.0, ACT["tanh"]) == 1.0
     assert oracle.act_prime(0.0, ACT["sigmoid"]) == 0.25
     for unknown in (7, 42, -2):  # unknown ids act as Linear
@@ -286,6 +291,89 @@ def test_set_unsigned_closed_form(oracle, dtype, qmax):
         assert oracle.set(dtype, r, s, i, n, float(v)) == 0
         assert _q_of(oracle, dtype, r, s, mn, n, i) == want, (DTYPE_NAMES[dtype], t, want)
         assert np.count_nonzero(r[:4] != raw[:4]) == 0  # the min header is kept
+
+
+# Uint32 (clamp to 4294967295.0 as f32 = 2^32, saturating conversion) and the
+# 64-bit unsigned formats (quant_u64 ops_storage.metal:106-113: 0 at or below
+# zero, 1e15 at or above 1e15f): (dtype, code bytes, largest code)
+UNSIGNED_WIDE = [(11, 4, 4294967295), (10, 8, 10**15), (22, 8, 10**15), (23, 8, 10**15)]
+
+
+@pytest.mark.parametrize("dtype,width,qtop", UNSIGNED_WIDE, ids=[DTYPE_NAMES[d] for d, _, _ in UNSIGNED_WIDE])
+def test_set_unsigned_wide_closed_form(oracle, dtype, width, qtop):
+    """The wide unsigned re-encode (ops_storage.metal:739-755, :826-858) read
+    back as the stored integer: with the stored min m and a power-of-two scale
+    s, small codes are round-half-away((v - m) / s) (an exact quotient, so only
+    the rounding rule decides: a truncation or ties-to-even fails), negative
+    quotients store 0, and huge values store the saturated top code."""
+    n, i = 16, 5
+    s, mn = 2.0 ** -4, -1.25
+    raw = np.zeros(oracle.native_bytes(dtype, n), np.uint8)
+    raw[:4] = np.frombuffer(np.float32(mn).tobytes(), np.uint8)
+    cases = [(q + 0.5, q + 1) for q in range(0, 8)]
+    cases += [(q + 0.5 - 2.0 ** -8, q) for q in range(0, 8)]
+    cases += [(q + 2.0 ** -8, q) for q in range(1, 8)]
+    cases += [(-0.5 + 2.0 ** -8, 0), (-0.5, 0), (-30.0, 0), (0.0, 0), (1000.5, 1001)]
+    dt = "<u4" if width == 4 else "<u8"
+    for t, want in cases + [(None, qtop)]:
+        r = raw.copy()
+        v = np.float32(1e30) if t is None else np.float32(mn + t * s)
+        if t is not None:
+            assert float(v) == mn + t * s
+        assert oracle.set(dtype, r, s, i, n, float(v)) == 0
+        got = int(r[4 + i * width:4 + (i + 1) * width].view(dt)[0])
+        assert got == want, (DTYPE_NAMES[dtype], t, got, want)
+        assert np.count_nonzero(r[:4] != raw[:4]) == 0
+        others = np.ones(r.size, bool)
+        others[4 + i * width:4 + (i + 1) * width] = False
+        assert not np.any(r[others] != raw[others])
+
+
+def _nf4_table(oracle):
+    codes = np.arange(16, dtype=np.uint8)
+    raw = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8)
+    return oracle.decode(26, raw, 1.0, 16)
+
+
+def _nf4_ties(table):
+    """f32 values r with |r - t[c]| == |r - t[c+1]| (both f32 differences) for
+    adjacent entries, found around each midpoint."""
+    ties = []
+    for c in range(15):
+        a, b = np.float32(table[c]), np.float32(table[c + 1])
+        mid = np.float32((np.float64(a) + np.float64(b)) / 2)
+        r = mid
+        for _ in range(64):
+            ea, eb = np.float32(abs(r - a)), np.float32(abs(r - b))
+            if ea == eb:
+                ties.append((c, float(r)))
+                break
+            r = np.nextafter(r, b if ea < eb else a, dtype=np.float32)
+    return ties
+
+
+def test_nf4_ties_go_to_the_first_index(oracle):
+    """NF4's nearest-entry search takes the first index on an exact tie of the
+    f32 distances, in the re-encode (ops_storage.metal:863-878) and in pack
+    (native_codec.cpp:93-110, scale 1 when the absmax is 1): values that sit
+    exactly between two adjacent table entries get the lower code, and the
+    values one f32 step to either side get the nearer one.  A `<=` search
+    (the last index wins) fails."""
+    table = _nf4_table(oracle)
+    ties = _nf4_ties(table)
+    assert len(ties) >= 5, ties
+    n, i = 8, 3
+    for c, r in ties:
+        for v, want in ((r, c), (float(np.nextafter(np.float32(r), np.float32(9), dtype=np.float32)), c + 1),
+                        (float(np.nextafter(np.float32(r), np.float32(-9), dtype=np.float32)), c)):
+            raw = np.zeros(n // 2, np.uint8)
+            assert oracle.set(26, raw, 1.0, i, n, v) == 0
+            assert (raw[i // 2] >> 4 * (i % 2)) & 0xF == want, (c, v, want)
+        # pack: absmax 1 fixes the scale at 1
+        w = np.zeros(n, np.float32)
+        w[0], w[i] = 1.0, r
+        raw, scale = oracle.pack(26, w)
+        assert scale == 1.0 and (raw[i // 2] >> 4 * (i % 2)) & 0xF == c, (c, r)
 
 
 @pytest.mark.parametrize("dtype,qmax", SIGNED_SET, ids=[DTYPE_NAMES[d] for d, _ in SIGNED_SET])
@@ -422,6 +510,24 @@ def test_mse_exact_rationals(oracle):
     for i in range(9):
         assert g[i] == rnd32(2 * (F(p[i]) - F(t[i])) / 9)
     assert oracle.mse(p, p) == 0.0 and not np.any(oracle.mse_grad(p, p))
+
+
+def test_mse_grad_rounds_once(oracle):
+    """grad = fl32(2 (p - t) / n) with the difference and quotient exact
+    before the one rounding (welvet_dense.metal:207-215: two_sum, then the
+    soft-double quotient): over inputs chosen so the difference p - t is not
+    an f32 (opposite signs, far-apart magnitudes), a gradient formed in f32
+    (rounded difference, rounded quotient) differs from the single rounding
+    in many places, and the oracle must match the single rounding in all."""
+    rng = np.random.default_rng(14)
+    n = 1536
+    p = (rng.normal(0, 1, n) * np.exp2(rng.integers(-6, 7, n))).astype(np.float32)
+    t = (-np.sign(p) * np.abs(rng.normal(0, 1, n)) * np.exp2(rng.integers(-14, -2, n))).astype(np.float32)
+    g = oracle.mse_grad(p, t)
+    want = np.array([rnd32(2 * (F(a) - F(b)) / n) for a, b in zip(p, t)], np.float32)
+    np.testing.assert_array_equal(g, want)
+    in_f32 = (np.float32(2) * (p - t)) / np.float32(n)
+    assert np.count_nonzero(in_f32 != want) >= 50
 
 
 # ------------------------------------------------------- CPU baseline path

@@ -405,8 +405,11 @@ __global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w
 // the launch (bad[k] != 0: store k's gradient holds a non-finite value), so
 // store c of the batch (index first + c in the sequence) is skipped when any
 // store k <= first + c is bad, exactly as a launch per store in sequence
-// order skips it; the first bad store records its code in *stop.  G: codes
-// per thread of the one-byte formats.
+// order skips it; the first bad store records its code in *stop.  The skip
+// rule reads only bad[], which no block of this launch writes: *stop is
+// written here but never read, since a block of a later bad store may set it
+// while blocks of earlier, good stores of the same launch are still to run.
+// G: codes per thread of the one-byte formats.
 template <int DT, int G>
 __global__ void __launch_bounds__(kThreads) sgd_batch_kernel(SgdBatch b, double lr, int *stop,
                                                              const int *bad, int first) {
@@ -426,7 +429,6 @@ __global__ void __launch_bounds__(kThreads) sgd_batch_kernel(SgdBatch b, double 
     if (fb == upto && blockIdx.x == 0 && threadIdx.x == 0) atomicCAS(stop, 0, t.code);
     return;
   }
-  if (*stop != 0) return;
   if constexpr (DT == kFloat32) sgd_f32_units((float *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
   else if constexpr (DT == kFloat64) sgd_f64_units((double *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
   else if constexpr (dtype_bits(DT) == 8 && fix_bytes<DT>() == 1)

@@ -58,8 +58,10 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
 // The SGD of up to kSgdBatch stores of one dtype in one launch, as
 // launch_sgd on each in sequence: store c is skipped when bad[k] != 0 for any
 // k <= first + c (its own gradient or an earlier store's is non-finite), and
-// the first such store sets *stop = its code if *stop was 0.  The stores'
-// parameters travel in the kernel arguments.
+// the first such store sets *stop = its code if *stop was 0.  The skip rule
+// reads bad[] only (never *stop), so a stop with another cause must end the
+// sequence before a batch is launched.  The stores' parameters travel in
+// the kernel arguments.
 constexpr int kSgdBatch = 16;
 struct SgdStore {
   uint8_t *body;

@@ -510,6 +510,10 @@ welvet_status grid_set_batch(welvet_hip_grid *g, int batch) {
       *p = nullptr;
       WH_HIP(hipMalloc(p, (size_t)batch * c.out * sizeof(float)));
     }
+    // the training gradient is [batch][out] too: the next step allocates it
+    // at the new batch (prepare_step)
+    if (c.grad) WH_HIP(hipFree(c.grad));
+    c.grad = nullptr;
   }
   g->batch = batch;  // the step buffers regrow on demand
   g->tape.clear();
@@ -577,11 +581,12 @@ welvet_status welvet_hip_volume_forward_device(welvet_hip_grid *g, const float *
     return make_status(kInvalid, "runtime.forward: output width %d, volume gives %d", out, out_w);
   const hipStream_t s = (hipStream_t)stream;
   // the last layer writes d_y itself (one copy command less per call) unless
-  // d_y overlaps that layer's input, which it still reads while writing
+  // d_y overlaps that layer's input, which it still reads while writing, or
+  // is not 16-byte aligned (the reduction epilogues store float4)
   const Grid::Cell &last = g->cells[g->tape.back()];
   const uintptr_t y0 = (uintptr_t)d_y, y1 = y0 + (size_t)g->batch * out * sizeof(float);
   const uintptr_t i0 = (uintptr_t)g->tape_in.back(), i1 = i0 + (size_t)g->batch * last.in * sizeof(float);
-  const bool direct = y1 <= i0 || i1 <= y0;
+  const bool direct = (y0 % 16 == 0) && (y1 <= i0 || i1 <= y0);
   st = run_forward(g, s, direct ? d_y : nullptr);
   if (st.code) return st;
   if (!direct)
