@@ -379,7 +379,10 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      most 8 waves, x of at most 128 registers per lane; the split-x
  *      formats' batch 5-8 up to 32 M weights):
  *      0 off, 1 on with an automatic grid, k >= 2 on with k waves per CU
- *      walking the row groups [1] */
+ *      walking the row groups [1]
+ *   21 batch <= 16 forward and dX without a k split (the no-split kernels
+ *      of knob 16): x / dpre copied into LDS once per workgroup when the
+ *      reduction length is at most 2048, 0 = each lane loads its own [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 /* No counterpart in the reference: a measurement aid.  Streams `bytes`

@@ -78,7 +78,8 @@ KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24)
          dict(bf3_cols=1, gemm_occ=1), dict(bf3_cols=2), dict(bf3_cols=2, bf3_small=1), dict(dw_mfma=0), dict(bf3_small=0),
          dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2), dict(bf3_groups=0),
          dict(bf3_depth=1), dict(bf3_groups=0, bf3_depth=2), dict(bf3_groups=1, gemm_occ=2),
-         dict(gemv_waves=-2), dict(gemv_waves=-3), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2)]
+         dict(gemv_waves=-2), dict(gemv_waves=-3), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2),
+         dict(regx=0), dict(regx=0, bf3_rows=2)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])

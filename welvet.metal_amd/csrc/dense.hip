@@ -1394,6 +1394,126 @@ __global__ void __launch_bounds__(64 * KG) gemm_regr_kernel(GemmArgs a, const do
   }
 }
 
+// gemm_regr_kernel with x in LDS, for K <= kRegxMaxK: the workgroup's
+// threads copy x [M][K] into LDS once, with contiguous 16-byte loads (1 KB per
+// wave load instruction), where gemm_regr_kernel's lanes each read 128
+// contiguous bytes of one x row per stage (64 cache lines per load
+// instruction: at 1024^2, batch 16, the loads took 2.5 of the kernel's 7 us).
+// The weights take a chunk-interleaved k order: chunk c of lane group h in
+// stage s holds k = s * ST + (4c + h) * E + e, so one chunk load of the wave
+// covers 64 contiguous bytes of each of its 16 rows; x is read from LDS in
+// the same order.  The first stage's weight loads are issued before the x
+// copy waits, so the two latencies overlap.  Rows of the LDS image past M and
+// columns past K are zero.  Dynamic LDS: 16 * (kRegxMaxK + 4) floats.
+constexpr int kRegxMaxK = 1024;
+template <int F, int KG>
+__global__ void __launch_bounds__(64 * KG) gemm_regx_kernel(GemmArgs a, const double *bias, int bias_len,
+                                                            int act, float *pre, float *post) {
+  using I = FI<F>;
+  using S = RegrShape<F>;
+  constexpr int E = S::E, W = I::kW, KR = S::KR, NCH = S::NCH, ST = S::ST;
+  typedef float floatx4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) float lut_s[I::kTable];
+  __shared__ float ex[KG - 1][4][64];
+  extern __shared__ __align__(16) float xs[];
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int j = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  constexpr int xp = kRegxMaxK + 4;  // LDS row pitch (floats); the image is kRegxMaxK wide
+  TabCopy<F> tab;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    __builtin_amdgcn_sched_barrier(0);  // issued before the x and weight loads
+  }
+  // x image [16][kRegxMaxK]: wave g copies rows g * RPW .. + RPW - 1, lane l
+  // the float4 columns l, l + 64, ...; loads from clamped in-range addresses,
+  // zero past M and K at the LDS store (no branches: every slot is written)
+  constexpr int RPW = 16 / KG, CPL = kRegxMaxK / 4 / 64;
+  float4 xv[RPW][CPL];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+      xv[r][i] = *(const float4 *)(a.A + (int64_t)min(g * RPW + r, a.M - 1) * a.K + min(4 * (lane + 64 * i), a.K - 4));
+  const int nrow = min(n0 + j, a.N - 1);
+  const bool nlive = n0 + j < a.N;
+  const uint8_t *wr = a.body + (int64_t)nrow * a.row_bytes;
+  const int nchunks = a.K / E;  // whole chunks of a row (K % E == 0 on this route)
+  struct Stage {
+    uint32_t w[NCH][W];
+  };
+  auto load = [&](Stage &st, int s) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = min(s * (ST / E) + 4 * c + h, nchunks - 1);
+      load_words<W>(wr + (int64_t)ch * (W * 4), st.w[c]);
+    }
+  };
+  Stage first;
+  load(first, min(g, a.nst - 1));
+  __builtin_amdgcn_sched_barrier(0);  // the x copy below waits for the x loads only
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int row = g * RPW + r, c4 = lane + 64 * i;
+      const bool ok = row < a.M && 4 * c4 < a.K;
+      *(float4 *)(xs + row * xp + 4 * c4) = ok ? xv[r][i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  if constexpr (I::kLut) tab.store(lut_s, tid);
+  lds_barrier();
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float *xrow = xs + j * xp;
+  auto compute = [&](const Stage &st, int s) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int k0 = s * ST + (4 * c + h) * E;
+      const bool ok = nlive && k0 < a.K;
+      float xk[E];
+      if constexpr (E >= 4) {
+#pragma unroll
+        for (int q = 0; q < E; q += 4) {
+          const float4 v = *(const float4 *)(xrow + k0 + q);
+          xk[q] = v.x; xk[q + 1] = v.y; xk[q + 2] = v.z; xk[q + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < E; ++q) xk[q] = xrow[k0 + q];
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float bv = ok ? (float)chunk_value<F>(st.w[c], e, lut_s, a.scale, a.minv) : 0.0f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xk[e], bv, acc, 0, 0, 0);
+      }
+    }
+  };
+  // a stage per wave in flight (one or two stages per wave at K <= 1024):
+  // the first was requested with x, the rest are loaded and used in turn
+  if (g < a.nst) compute(first, g);
+  for (int s = g + KG; s < a.nst; s += KG) {
+    Stage st;
+    load(st, s);
+    compute(st, s);
+  }
+  // D[4h + r][j] of the tile: groups 1.. hand theirs to group 0
+  if (g > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ex[g - 1][r][lane] = acc[r];
+  }
+  lds_barrier();
+  if (g != 0) return;
+  const int n = n0 + j;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * h + r;
+    double sum = (double)acc[r];
+#pragma unroll
+    for (int q = 0; q < KG - 1; ++q) sum += (double)ex[q][r][lane];
+    if (a.post != 1.0f) sum *= (double)a.post;
+    if (m < a.M && n < a.N) bias_act_store(sum, n, bias, bias_len, act, pre, post, (int64_t)m * a.N + n);
+  }
+}
+
 // dX of the fp32-MFMA formats at batch <= 16, rows <= 2048, without a k
 // split: dX[b][i] = sum_o dpre[b][o] W[o][i] as gemm_regr_kernel's product
 // through W^T.  A wave owns 16 output columns i (n0..n0+15) and walks stages
@@ -1420,7 +1540,11 @@ struct RegtShape {
 // (act_deriv_kernel's expression on the stored dX, so the same bits), so
 // that layer's backward needs no derivative launch.  next_pre is loaded with
 // the first stage, off the epilogue's critical path.
-template <int F, int KG, bool NEXT>
+// XL: dpre [M][K] is copied into (dynamic) LDS once per workgroup with
+// contiguous 16-byte loads, as in gemm_regx_kernel, instead of each lane
+// loading its KR rows' values per stage; rows past M and past K are zero.
+constexpr int kRegtxMaxK = 1024;
+template <int F, int KG, bool NEXT, bool XL = false>
 __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *out, const float *next_pre,
                                                             int next_act) {
   using I = FI<F>;
@@ -1442,6 +1566,20 @@ __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *o
   const int mrow = min(m0 + j, a.M - 1);
   const bool mlive = m0 + j < a.M;
   const float *xr = a.A + (int64_t)mrow * a.K;
+  extern __shared__ __align__(16) float xs[];
+  constexpr int xp = kRegtxMaxK + 4;  // XL: LDS row pitch (floats), image kRegtxMaxK wide
+  // XL: wave g copies rows g * RPW .. + RPW - 1 of dpre, lane l the float4
+  // columns l, l + 64, ... (as gemm_regx_kernel)
+  constexpr int RPW = 16 / KG, CPL = XL ? kRegtxMaxK / 4 / 64 : 1;
+  float4 xv4[RPW][CPL];
+  if constexpr (XL) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i)
+        xv4[r][i] = *(const float4 *)(a.A + (int64_t)min(m0 + g * RPW + r, a.M - 1) * a.K +
+                                      min(4 * (lane + 64 * i), a.K - 4));
+  }
   // chunk load c of this lane: row r = q / CPR, chunk cc = q % CPR of the
   // piece (q = lane + 64 c); column chunk index along the stored row
   int lr[NCH], lcol[NCH];
@@ -1458,10 +1596,12 @@ __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *o
   };
   auto load = [&](Stage &st, int s) {
     const int k0 = s * ST;
+    if constexpr (!XL) {
 #pragma unroll
-    for (int q = 0; q < KR; q += 4) {
-      const float4 v = *(const float4 *)(xr + min(k0 + KR * h + q, a.K - 4));
-      st.x[q] = v.x; st.x[q + 1] = v.y; st.x[q + 2] = v.z; st.x[q + 3] = v.w;
+      for (int q = 0; q < KR; q += 4) {
+        const float4 v = *(const float4 *)(xr + min(k0 + KR * h + q, a.K - 4));
+        st.x[q] = v.x; st.x[q + 1] = v.y; st.x[q + 2] = v.z; st.x[q + 3] = v.w;
+      }
     }
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -1495,14 +1635,36 @@ __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *o
   floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](const Stage &st, int s) {
     const int k0 = s * ST + KR * h;
+    float xl[KR];
+    if constexpr (XL) {
+#pragma unroll
+      for (int q = 0; q < KR; q += 4) {
+        const float4 v = *(const float4 *)(xs + j * xp + k0 + q);
+        xl[q] = v.x; xl[q + 1] = v.y; xl[q + 2] = v.z; xl[q + 3] = v.w;
+      }
+    }
 #pragma unroll
     for (int t = 0; t < KR; ++t) {
-      const float xv = (mlive && k0 + (t & ~3) < a.K) ? st.x[t] : 0.0f;
+      float xv;
+      if constexpr (XL) xv = xl[t];
+      else xv = (mlive && k0 + (t & ~3) < a.K) ? st.x[t] : 0.0f;
       acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv, tw[(KR * h + t) * P + j], acc, 0, 0, 0);
     }
   };
   Stage cur, nxt;
   load(cur, min(g, a.nst - 1));
+  if constexpr (XL) {
+    __builtin_amdgcn_sched_barrier(0);  // the copy below waits for the dpre loads only
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int row = g * RPW + r, c4 = lane + 64 * i;
+        const bool ok = m0 + row < a.M && 4 * c4 < a.K;
+        *(float4 *)(xs + row * xp + 4 * c4) = ok ? xv4[r][i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    if constexpr (!I::kLut) lds_barrier();
+  }
   float np[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (NEXT) {
     if (g == 0) {  // the storing wave's four outputs, clamped in range
@@ -1515,17 +1677,37 @@ __global__ void __launch_bounds__(64 * KG) gemm_regt_kernel(GemmArgs a, float *o
     tab.store(lut_s, tid);
     lds_barrier();
   }
-  for (int s = g; s < a.nst; s += KG) {
-    load(nxt, min(s + KG, a.nst - 1));
-    // LDS operations of one wave complete in order: the previous stage's
-    // tile reads are done before these writes, and the writes before the
-    // reads below; the clobbers keep the compiler from reordering them
-    asm volatile("" ::: "memory");
-    put(cur, s);
-    asm volatile("" ::: "memory");
-    compute(cur, s);
-    asm volatile("" ::: "memory");
-    cur = nxt;
+  // LDS operations of one wave complete in order: the previous stage's tile
+  // reads are done before the next writes, and the writes before the reads;
+  // the clobbers keep the compiler from reordering them
+  if constexpr (XL) {
+    // dpre in LDS: a stage per wave in flight (the first requested with
+    // dpre), the rest loaded and used in turn
+    if (g < a.nst) {
+      asm volatile("" ::: "memory");
+      put(cur, g);
+      asm volatile("" ::: "memory");
+      compute(cur, g);
+      asm volatile("" ::: "memory");
+    }
+    for (int s = g + KG; s < a.nst; s += KG) {
+      load(nxt, s);
+      asm volatile("" ::: "memory");
+      put(nxt, s);
+      asm volatile("" ::: "memory");
+      compute(nxt, s);
+      asm volatile("" ::: "memory");
+    }
+  } else {
+    for (int s = g; s < a.nst; s += KG) {
+      load(nxt, min(s + KG, a.nst - 1));
+      asm volatile("" ::: "memory");
+      put(cur, s);
+      asm volatile("" ::: "memory");
+      compute(cur, s);
+      asm volatile("" ::: "memory");
+      cur = nxt;
+    }
   }
   if (g > 0) {
 #pragma unroll
@@ -2878,7 +3060,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1, 1, 1};
+int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1, 1, 1, 1};
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -3274,6 +3456,37 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
 // occupancy query), but at least two row groups per block, so the prefetch
 // has a next group (measured on FP8, FP4 and NF4 at 4096^2, 4096 -> 11008
 // and 11008 -> 4096: it picks the best of 4, 8, 12 and 16 waves per CU).
+// gemm_regx_kernel for plan p: dynamic LDS for the x image, allowed past the
+// default per-launch limit once per kernel.
+template <int F>
+hipError_t launch_regx(const SkPlan &p, const GemmArgs &a, const double *bias, int bias_len, int act,
+                       float *pre, float *post, hipStream_t s) {
+  constexpr size_t lds = (size_t)16 * (kRegxMaxK + 4) * sizeof(float);
+  static const hipError_t attr = hipFuncSetAttribute((const void *)gemm_regx_kernel<F, 8>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  gemm_regx_kernel<F, 8><<<dim3(p.gx, p.gy), 512, lds, s>>>(a, bias, bias_len, act, pre, post);
+  return hipGetLastError();
+}
+
+// gemm_regt_kernel with dpre in LDS (batch <= 16, rows <= kRegtxMaxK).
+template <int F>
+hipError_t launch_regtx(const GemmArgs &a, float *dX, const float *next_pre, int next_act, hipStream_t s) {
+  constexpr int kMax = (int)(16 * (kRegtxMaxK + 4) * sizeof(float));
+  static const hipError_t attr_t = hipFuncSetAttribute((const void *)gemm_regt_kernel<F, 8, true, true>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
+  static const hipError_t attr_f = hipFuncSetAttribute((const void *)gemm_regt_kernel<F, 8, false, true>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMax);
+  if (attr_t != hipSuccess) return attr_t;
+  if (attr_f != hipSuccess) return attr_f;
+  constexpr size_t lds = kMax;
+  if (next_pre != nullptr)
+    gemm_regt_kernel<F, 8, true, true><<<dim3(a.gx, a.gy), 512, lds, s>>>(a, dX, next_pre, next_act);
+  else
+    gemm_regt_kernel<F, 8, false, true><<<dim3(a.gx, a.gy), 512, lds, s>>>(a, dX, nullptr, -1);
+  return hipGetLastError();
+}
+
 template <int F, int C, int R, int B>
 hipError_t launch_loopb(const GemvArgs &a, int batch, int S, hipStream_t s) {
   const int ngroups = (a.N + R - 1) / R;
@@ -3515,6 +3728,8 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
     if (e != hipSuccess) return e;
   } else if (p.rows) {
 #define WH_GRR(F)                                                                                     \
+  if (batch <= 16 && w.cols <= kRegxMaxK && g_tune[kTuneRegx] != 0)                                   \
+    return launch_regx<F>(p, a, bias, bias_len, act, pre, post, s);                                   \
   gemm_regr_kernel<F, 8><<<dim3(p.gx, p.gy), 512, 0, s>>>(a, bias, bias_len, act, pre, post);          \
   break;
     WH_FMT_SWITCH(f, WH_GRR)
@@ -3702,6 +3917,11 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
                (w.cols + 15) / 16, (batch + 15) / 16, (w.rows + st - 1) / st, 0, 1, nullptr, 16, 16};
 #define WH_DXR(F)                                                                                   \
+  if (batch <= 16 && w.rows <= kRegtxMaxK && g_tune[kTuneRegx] != 0) {                              \
+    e = launch_regtx<F>(a, dX, chain.dx_next_pre, chain.dx_next_act, s);                            \
+    if (e != hipSuccess) return e;                                                                  \
+    break;                                                                                          \
+  }                                                                                                 \
   if (chain.dx_next_pre != nullptr)                                                                 \
     gemm_regt_kernel<F, 8, true><<<dim3(a.gx, a.gy), 512, 0, s>>>(a, dX, chain.dx_next_pre,          \
                                                                   chain.dx_next_act);               \

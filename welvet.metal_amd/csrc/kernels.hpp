@@ -189,13 +189,15 @@ void set_forward_path(int path);
 // training step, the SGD of consecutive stores of one dtype in one launch
 // (up to kSgdBatch per launch; 1 on, 0 one launch per store).  19 in a
 // volume training step, the dW of every layer deferred to the end of the
-// backward and launched kDwBatch layers at a time (1 on).
+// backward and launched kDwBatch layers at a time (1 on).  21 the batch <= 16
+// no-split forward and dX with x / dpre copied into LDS once per workgroup
+// (K <= 2048; 1 on).
 enum TuneKey {
   kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
   kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
   kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
   kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kTuneDwBatch = 19,
-  kTuneGemvBatch = 20, kNumTune = 21
+  kTuneGemvBatch = 20, kTuneRegx = 21, kNumTune = 22
 };
 int set_tuning(int key, int value);
 int tuning(int key);  // the current value (-1 for an unknown key)
