@@ -320,43 +320,16 @@ WELVET_API void welvet_hip_swiglu_release(welvet_hip_swiglu *s);
 
 /* Kernel route of the forward: 0 auto, 1 GEMV, 2 MFMA GEMM, 3 element-wise. */
 WELVET_API void welvet_hip_set_forward_path(int32_t path);
-/* Kernel tuning knob `key` := value, returns the previous value (-1 = unknown
- * key).  Process-wide; results stay within the same tolerance whatever the
- * setting.  Keys (default in brackets):
- *   0 batch-1 GEMV kernel: 0 row-group, 1 all-loads-in-flight [1],
- *     2 column-stationary
- *   1 column-stationary rows per block [0 = 16]
- *   2 column-stationary in-lane f64 accumulation [0]
- *   3 all-loads-in-flight chunks per lane: 0 auto, 1 two, 2 four, 3 one,
- *     4 eight [0]
- *   4 register-B MFMA GEMM for formats of <= 16 bits [1]
- *   5 its workgroups per CU [0 = 2]
- *   6 hardware FP8 / FP4 conversions and integer Int8 decode instead of
- *     tables [1]
- *   7 byte-pair decode table for 4-bit formats [1]
- *   8 all-loads-in-flight rows per block: 0 = 8 / chunks per lane, or 1, 2,
- *     4, 8, 16 (at most 16 / chunks per lane; FP8, Int8, 4-bit, 8-bit table
- *     and half formats) [0]
- *   9 all-loads-in-flight grid: waves per CU walking the row groups, 0 = one
- *     block per row group, -1 = auto (16 for FP8 E4M3/E5M2 and FP4 and for
- *     NF4 rows of at most 4096 inputs, 12 for NF4 rows of 5-8 waves, one
- *     block per group for FP8 rows of 5-8 waves of two chunks, else 0),
- *     -k (k >= 2) = k row groups per block [-1]
+/* Route switch `key` := value, returns the previous value (-1 = unknown key,
+ * the value unchanged).  Process-wide and atomic: a call on one thread is seen
+ * by launches on any other, and a launch reads each switch once.  Every
+ * setting computes the same result within the same tolerance (dW and the
+ * SGD bit for bit); the switches exist so that tests can compare routes and
+ * sweeps can time them.  Keys (default in brackets; the other key numbers
+ * are unknown):
  *   10 split-x bf16 MFMA GEMM (x split exactly into three bf16 parts) for
- *     FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4 [1]
- *   11 its weight prefetch depth in k stages: 0 auto (1; 2 on the two-group
- *      workgroups of key 15), 1, 2, or 3 (batch <= 32) [0]
- *   12 its block width: 0 auto (128 output columns for at most 8192
- *      outputs on the 16-row tile and on the one-byte kinds' 32-row tile,
- *      else 256), 1 = 128, 2 = 256 [0]
- *   13 dW kernel, every one bit-identical to the sequential FMA (the fp32
- *      MFMA accumulates each product with fmaf rounding, in k order): 2 MFMA
- *      with operands staged in LDS (out and in multiples of 128, else 1),
- *      1 MFMA with direct loads, 0 VALU [2]
- *   14 split-x GEMM for batch <= 16 on a 16-row tile (16x16x32 MFMA) instead
- *      of the 32-row one [1]
- *   15 split-x GEMM on 8-wave workgroups whose two wave groups share each
- *      unit's k range (one partial tile per workgroup) [1]
+ *      FP8 E4M3 / E5M2, Int8, FP4 and NF4 weights at batch > 4, 0 = the
+ *      fp32 MFMA GEMMs [1]
  *   16 batch <= 16 forward and dX without a k split across workgroups
  *      (epilogue in the kernel, no reduction launch; the split-x GEMM for
  *      its formats, the fp32 MFMA for the others): 0 off, 1 for a
@@ -380,9 +353,9 @@ WELVET_API void welvet_hip_set_forward_path(int32_t path);
  *      formats' batch 5-8 up to 32 M weights):
  *      0 off, 1 on with an automatic grid, k >= 2 on with k waves per CU
  *      walking the row groups [1]
- *   21 batch <= 16 forward and dX without a k split (the no-split kernels
- *      of knob 16): x / dpre copied into LDS once per workgroup when the
- *      reduction length is at most 2048, 0 = each lane loads its own [1] */
+ *   21 the fp32-MFMA no-split forward and the no-split dX of key 16 with x /
+ *      dpre copied into LDS once per workgroup when the reduction length is
+ *      at most 1024, 0 = each lane loads its own [1] */
 WELVET_API int32_t welvet_hip_set_tuning(int32_t key, int32_t value);
 
 /* No counterpart in the reference: a measurement aid.  Streams `bytes`

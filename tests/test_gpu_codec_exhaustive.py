@@ -104,15 +104,13 @@ def test_export_decodes_every_code(oracle, dtype):
 
 # Knob sets that route the forward through each decode: the default kernels
 # (hardware FP8 / FP4 converts, the byte-pair NF4 table, the split-x GEMM),
-# the table decodes, the fp32 MFMA GEMMs and the element-wise kernel.
+# the k-split GEMMs that default to the no-split ones at these shapes, the
+# fp32 MFMA GEMMs and the element-wise kernel.
 ROUTES = {
     "default": {},
-    "tables": dict(fast_decode=0, pair_lut=0),
-    "pair_table_no_fast": dict(fast_decode=0),
+    "k_split": dict(bf3_rows=0),
     "no_split_x": dict(bf3=0),
-    "lds_gemm": dict(bf3=0, reg_gemm=0),
-    "gemv_rowgroup": dict(gemv1=0),
-    "gemv_column_stationary": dict(gemv1=2),
+    "no_split_x_k_split": dict(bf3=0, bf3_rows=0),
     "elementwise": "path3",
 }
 

@@ -64,27 +64,13 @@ def test_forward_each_route(oracle, dtype, path):
     check_forward(oracle, dtype, W, x, path=path)
 
 
-KNOBS = [dict(gemv1=0), dict(gemv1=2), dict(gemv1=2, acc64=1, rows_per_block=24), dict(cr=1),
-         dict(cr=2), dict(cr=3), dict(cr=4), dict(reg_gemm=0), dict(gemm_occ=4),
-         dict(fast_decode=0, pair_lut=0), dict(fast_decode=1), dict(pair_lut=1),
-         dict(fast_decode=1, pair_lut=1, gemv1=0), dict(fast_decode=1, pair_lut=1, reg_gemm=0),
-         dict(gemv_rows=1), dict(gemv_rows=2), dict(gemv_rows=4), dict(gemv_rows=2, cr=1),
-         dict(gemv_rows=1, cr=2), dict(gemv_rows=1, pair_lut=0, fast_decode=0),
-         dict(gemv_rows=16, cr=3), dict(gemv_rows=8, cr=1), dict(gemv_rows=16, cr=3, pair_lut=0),
-         dict(gemv_waves=0), dict(gemv_waves=1), dict(gemv_waves=12), dict(gemv_waves=1, cr=1),
-         dict(gemv_waves=2, gemv_rows=16, cr=3), dict(gemv_waves=1, gemv_rows=1, pair_lut=0),
-         dict(bf3=0), dict(bf3=1, gemm_occ=1), dict(bf3=1, gemm_occ=4), dict(bf3_depth=2),
-         dict(bf3_depth=3), dict(bf3_depth=3, gemm_occ=1), dict(bf3_cols=1),
-         dict(bf3_cols=1, gemm_occ=1), dict(bf3_cols=2), dict(bf3_cols=2, bf3_small=1), dict(dw_mfma=0), dict(bf3_small=0),
-         dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2), dict(bf3_groups=0),
-         dict(bf3_depth=1), dict(bf3_groups=0, bf3_depth=2), dict(bf3_groups=1, gemm_occ=2),
-         dict(gemv_waves=-2), dict(gemv_waves=-3), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2),
-         dict(regx=0), dict(regx=0, bf3_rows=2)]
+KNOBS = [dict(), dict(bf3=0), dict(bf3_rows=0), dict(bf3_rows=2), dict(regx=0),
+         dict(regx=0, bf3_rows=2), dict(bf3=0, bf3_rows=0), dict(gemv_batch=0)]
 
 
 @pytest.mark.parametrize("knobs", KNOBS, ids=[",".join(f"{k}={v}" for k, v in d.items()) for d in KNOBS])
 def test_forward_kernel_variants(oracle, knobs):
-    """Every kernel variant the tuning knobs reach gives the same parity."""
+    """Every route the tuning knobs select gives the same parity."""
     old = {k: pywelvet.set_tuning(k, v) for k, v in knobs.items()}
     try:
         rng = np.random.default_rng(21)
@@ -115,30 +101,25 @@ def test_split_x_two_group_workgroups(oracle, dtype):
     alternate k stages and add their sums through LDS at each tile's end:
     64-row tiles (batch 33-64, ragged batch included) and the 32-row tiles of
     the 4-bit kinds, K whose last stage runs past it, shares crossing tile
-    boundaries, both ring depths, and the dX of a forward through the
-    transposed codes (K = rows)."""
+    boundaries, and the dX of a forward through the transposed codes (K =
+    rows)."""
     rng = np.random.default_rng(1500 + dtype)
     cases = ((300, 2016, 64), (257, 1024, 48), (128, 4096, 33), (1000, 512, 64), (300, 2016, 20))
-    for depth in (0, 1):
-        old = pywelvet.set_tuning("bf3_depth", depth)
-        try:
-            for out, inn, batch in cases:
-                W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
-                if dtype == 16:
-                    W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
-                x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
-                check_forward(oracle, dtype, W, x, act=2, bias=rng.normal(0, 0.1, out))
-            W = rng.normal(0, 0.1, (384, 640)).astype(np.float32)
-            x = rng.normal(0, 1, (40, 640)).astype(np.float32)
-            gy = rng.normal(0, 1, (40, 384)).astype(np.float32)
-            pre = rng.normal(0, 1, (40, 384)).astype(np.float32)
-            with pywelvet.Session(W, batch=40, act=-1, dtype=dtype) as s:
-                dX, dW = s.backward(x, pre, gy)
-            _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, -1)
-            assert_close(dX, rdX, 384, f"dX depth {depth}")
-            assert_bit_equal(dW, rdW, f"dW depth {depth}")
-        finally:
-            pywelvet.set_tuning("bf3_depth", old)
+    for out, inn, batch in cases:
+        W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
+        if dtype == 16:
+            W = rng.uniform(-6, 6, (out, inn)).astype(np.float32)
+        x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+        check_forward(oracle, dtype, W, x, act=2, bias=rng.normal(0, 0.1, out))
+    W = rng.normal(0, 0.1, (384, 640)).astype(np.float32)
+    x = rng.normal(0, 1, (40, 640)).astype(np.float32)
+    gy = rng.normal(0, 1, (40, 384)).astype(np.float32)
+    pre = rng.normal(0, 1, (40, 384)).astype(np.float32)
+    with pywelvet.Session(W, batch=40, act=-1, dtype=dtype) as s:
+        dX, dW = s.backward(x, pre, gy)
+    _, rdX, rdW = oracle.backward(oracle_weights(oracle, dtype, W), x, pre, gy, -1)
+    assert_close(dX, rdX, 384, "dX")
+    assert_bit_equal(dW, rdW, "dW")
 
 
 @pytest.mark.parametrize("dtype", [16, 26, 14, 15, 4, 5])
@@ -161,9 +142,9 @@ def test_long_row_gemv(oracle, dtype, cols):
 @pytest.mark.parametrize("batch", [5, 8, 13, 16, 17])
 def test_split_x_small_batch_tile(oracle, dtype, batch):
     """The split-x GEMM's 16-row tile (16x16x32 MFMA, batch <= 16) and the
-    32-row tile it replaces: ragged N (304 rows), K not a multiple of the 64-deep stage,
-    both block widths and prefetch depths, forward and the dX that runs
-    through the store's transposed codes."""
+    no-split 16-row kernel that replaces it by default: ragged N (304 rows), K
+    not a multiple of the 64-deep stage, forward and the dX that runs through
+    the store's transposed codes."""
     rng = np.random.default_rng(1300 + 17 * dtype + batch)
     W = rng.normal(0, 0.1, (304, 1040)).astype(np.float32)
     if dtype == 16:
@@ -173,8 +154,7 @@ def test_split_x_small_batch_tile(oracle, dtype, batch):
     pre = rng.normal(0, 1, (batch, 304)).astype(np.float32)
     Wd = oracle_weights(oracle, dtype, W)
     _, rdX, rdW = oracle.backward(Wd, x, pre, gy, -1)
-    for knobs in (dict(bf3_small=1), dict(bf3_small=1, bf3_cols=1), dict(bf3_small=1, bf3_depth=2),
-                  dict(bf3_small=0), dict(bf3_rows=0), dict(bf3_rows=2), dict(bf3_rows=2, bf3_depth=2)):
+    for knobs in (dict(), dict(bf3_rows=0), dict(bf3_rows=2)):
         old = {k: pywelvet.set_tuning(k, v) for k, v in knobs.items()}
         try:
             check_forward(oracle, dtype, W, x)
@@ -238,46 +218,29 @@ def test_no_split_gemm_wide_outputs(oracle, dtype):
         check_forward(oracle, dtype, W, x)
 
 
-def test_every_gemv_shape_knob_launches(oracle):
-    """Every (chunks per lane, rows per block) request, including ones with
-    no kernel of their own, computes the forward (falls back, never skips)."""
-    rng = np.random.default_rng(23)
-    cases = [(4, 300, 1024), (26, 257, 2048), (9, 64, 4096), (2, 40, 3072), (16, 130, 2048)]
-    old = {k: pywelvet.set_tuning(k, 0) for k in ("cr", "gemv_rows")}
-    try:
-        for cr in range(5):
-            for rows in (0, 1, 2, 3, 4, 8, 16, 32):
-                pywelvet.set_tuning("cr", cr)
-                pywelvet.set_tuning("gemv_rows", rows)
-                for dtype, out, inn in cases:
-                    W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
-                    x = rng.normal(0, 1, (1, inn)).astype(np.float32)
-                    check_forward(oracle, dtype, W, x)
-    finally:
-        for k, v in old.items():
-            pywelvet.set_tuning(k, v)
+# (dtype, rows, cols) whose batch-1 GEMV takes the fixed-grid loop with a
+# partial last row group: FP8 at one chunk per lane and 4 rows per group
+# (4096 inputs, 2752 groups over 1024 blocks) and at two chunks per lane
+# (8192 inputs, 1025 groups over 1024 blocks), FP4 at 8 rows per group (4096
+# inputs, 2501 groups over 2048 blocks), NF4 at one chunk per lane over 2
+# waves (4096 inputs) and over 6 waves at 12 waves per CU (11008 inputs, 1025
+# groups over 512 blocks)
+LOOP_CASES = [(4, 11007, 4096), (4, 4099, 8192), (5, 11007, 4096), (16, 20003, 4096),
+              (26, 11007, 4096), (26, 4097, 11008)]
 
 
-@pytest.mark.parametrize("dtype", [4, 5, 16, 26])
-def test_loop_gemv_ragged_rows(oracle, dtype):
-    """The fixed-grid batch-1 GEMV (several row groups per block) for every
-    (chunks per lane, rows per block) it is built for, on row counts that
-    leave a partial last group and on blocks that walk 2 or 3 groups."""
-    rng = np.random.default_rng(29 + dtype)
-    names = ("cr", "gemv_rows", "gemv_waves")
-    old = {k: pywelvet.set_tuning(k, 0) for k in names}
-    try:
-        for cr, rows in ((3, 4), (3, 8), (3, 2), (1, 4)):
-            for waves in (-2, -3):
-                for k, v in zip(names, (cr, rows, waves)):
-                    pywelvet.set_tuning(k, v)
-                for out, inn in ((203, 4096), (11, 1024), (37, 2048)):
-                    W = rng.normal(0, 0.1, (out, inn)).astype(np.float32)
-                    x = rng.normal(0, 1, (1, inn)).astype(np.float32)
-                    check_forward(oracle, dtype, W, x)
-    finally:
-        for k, v in old.items():
-            pywelvet.set_tuning(k, v)
+@pytest.mark.parametrize("dtype,rows,cols", LOOP_CASES,
+                         ids=[f"{DTYPE_NAMES[d]}-{r}x{c}" for d, r, c in LOOP_CASES])
+def test_loop_gemv_ragged_rows(oracle, dtype, rows, cols):
+    """The fixed-grid batch-1 GEMV (blocks walking several row groups) on
+    the shapes that select it, with a partial last group."""
+    rng = np.random.default_rng(29 + dtype + rows)
+    if dtype == 16:
+        W = rng.uniform(-6, 6, (rows, cols)).astype(np.float32)
+    else:
+        W = rng.normal(0, 0.05, (rows, cols)).astype(np.float32)
+    x = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    check_forward(oracle, dtype, W, x, act=1, bias=rng.normal(0, 0.1, rows))
 
 
 @pytest.mark.parametrize("dtype", [4, 26, 2, 7])
@@ -463,6 +426,46 @@ def test_forward_after_sgd_reads_updated_store(oracle, dtype, batch):
             assert_close(pre, rpre, inn, f"{DTYPE_NAMES[dtype]} step {step}")
 
 
+def assert_same_nonfinite(got, want, k, label):
+    """NaN where want has NaN, the same infinities, finite values within the
+    tolerance for a length-k reduction."""
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want), err_msg=f"{label} NaN")
+    inf = np.isinf(want)
+    np.testing.assert_array_equal(np.where(inf, got, 0), np.where(inf, want, 0), err_msg=f"{label} Inf")
+    fin = np.isfinite(want)
+    assert_close(np.where(fin, got, 0), np.where(fin, want, 0), k, f"{label} finite")
+
+
+@pytest.mark.parametrize("batch", [8, 40])
+def test_e5m2_finiteness_follows_sgd(oracle, batch):
+    """An E5M2 store's Inf / NaN status is re-read from the codes each SGD
+    writes: an update that stays finite keeps the store on the split-x GEMM,
+    one that pushes weights past the format's range (Inf codes) moves the
+    forward and dX off it.  Each matches the oracle on the exported weights,
+    non-finite outputs identical in class; dW bit for bit."""
+    rng = np.random.default_rng(4100 + batch)
+    out, inn = 96, 512
+    W = rng.normal(0, 0.05, (out, inn)).astype(np.float32)
+    with pywelvet.Session(W, batch=batch, act=-1, dtype=5) as s:
+        for step in range(2):
+            g = rng.normal(0, 1, (out, inn)).astype(np.float32)
+            if step == 1:
+                g[5, 17], g[60, 300] = -1e9, 1e9  # lr * g = -+1e6, past E5M2's range
+            s.sgd(g, 1e-3)
+            Wd = s.export_f32().astype(np.float64)
+            assert bool(np.isfinite(Wd).all()) == (step == 0)
+            x = rng.normal(0, 1, (batch, inn)).astype(np.float32)
+            pre, _ = s.execute(x)
+            rpre, _ = oracle.forward(Wd, x, -1)
+            assert_same_nonfinite(pre, rpre, inn, f"forward step {step}")
+            gy = rng.normal(0, 1, (batch, out)).astype(np.float32)
+            bpre = rng.normal(0, 1, (batch, out)).astype(np.float32)
+            dX, dW = s.backward(x, bpre, gy)
+            _, rdX, rdW = oracle.backward(Wd, x, bpre, gy, -1)
+            assert_same_nonfinite(dX, rdX, out, f"dX step {step}")
+            assert_bit_equal(dW, rdW, f"dW step {step}")
+
+
 @pytest.mark.parametrize("dtype", [4, 26, 1])
 def test_gemm_session_repeat(oracle, dtype):
     """Repeated MFMA launches on one session reuse its stream-K workspace:
@@ -510,7 +513,8 @@ def test_backward(oracle, dtype, batch):
 @pytest.mark.parametrize("batch", [1, 2, 3, 7, 64, 65])
 def test_dw_bit_exact_special_values(oracle, batch, shape):
     """dW stays the reference's sequential fmaf over the batch, bit for bit,
-    on every dW kernel (LDS-staged MFMA, direct MFMA, VALU), with signed zeros
+    on both dW kernels (LDS-staged MFMA for whole 128-tiles, direct MFMA for
+    ragged shapes), with signed zeros
     (ReLU passes -0 gradients), denormal inputs and products across the
     exponent range, odd and even batches, ragged and whole 128-tiles."""
     rng = np.random.default_rng(131 + batch)
@@ -525,17 +529,11 @@ def test_dw_bit_exact_special_values(oracle, batch, shape):
     gy[:, 2::9] *= np.float32(1e-25)
     pre = rng.normal(0, 1, (batch, out)).astype(np.float32)
     Wd = oracle_weights(oracle, 1, W)
-    old = pywelvet.set_tuning("dw_mfma", 1)
-    try:
-        for knob in (2, 1, 0):
-            pywelvet.set_tuning("dw_mfma", knob)
-            for act in (-1, 0):
-                with pywelvet.Session(W, batch=batch, act=act, dtype=1) as s:
-                    _, dW = s.backward(x, pre, gy)
-                _, _, rdW = oracle.backward(Wd, x, pre, gy, act)
-                assert_bit_equal(dW, rdW, f"dW dw_mfma={knob} act={act}")
-    finally:
-        pywelvet.set_tuning("dw_mfma", old)
+    for act in (-1, 0):
+        with pywelvet.Session(W, batch=batch, act=act, dtype=1) as s:
+            _, dW = s.backward(x, pre, gy)
+        _, _, rdW = oracle.backward(Wd, x, pre, gy, act)
+        assert_bit_equal(dW, rdW, f"dW act={act}")
 
 
 def test_backward_ragged(oracle):

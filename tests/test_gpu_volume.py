@@ -357,6 +357,43 @@ def test_train_batched_sgd_and_dw_match_per_cell(oracle, dtypes, widths, xs, lr)
             assert_bit_equal(runs[knobs][1][co], runs[(1, 1)][1][co], f"store {co} knobs {knobs}")
 
 
+@pytest.mark.parametrize("sgd_batch", [1, 0])
+def test_train_e5m2_overflow_then_forward(oracle, sgd_batch):
+    """E5M2 cells after training steps, batch 8 (where a finite E5M2 store
+    takes the split-x GEMM): a step that stays finite, then one whose update
+    pushes weights past the format's range (Inf codes).  After each, the
+    stores are read back into the oracle and the next forward keeps the IEEE
+    results: NaN and Inf where the oracle has them, finite outputs within
+    tolerance."""
+    rng = np.random.default_rng(2700 + sgd_batch)
+    spec = {(0, 0, 0, 0): (rng.normal(0, 0.1, (128, 128)).astype(np.float32), 0, 5, None),
+            (0, 0, 0, 1): (rng.normal(0, 0.1, (64, 128)).astype(np.float32), -1, 5, None)}
+    x = rng.normal(0, 1, (8, 128)).astype(np.float32)
+    t = rng.normal(0, 1, (8, 64)).astype(np.float32)
+    old = pywelvet.set_tuning("sgd_batch", sgd_batch)
+    try:
+        G, V = build(oracle, (1, 1, 1, 2), 8, spec)
+        with G:
+            # lr 1e6: about 0.1% of the top layer's codes go to Inf (oracle)
+            for step, lr in enumerate((1e-2, 1e6)):
+                G.train_step(x, t, lr)
+                for co in spec:
+                    V.cells[co]["raw"] = G.native(co)[0].copy()
+                finite = all(np.isfinite(G.export_f32(co)).all() for co in spec)
+                assert finite == (step == 0), step
+                x2 = rng.normal(0, 1, (8, 128)).astype(np.float32)
+                y = G.forward(x2, 64)
+                code, _, ry, _ = V.forward(x2)
+                assert code == 0
+                np.testing.assert_array_equal(np.isnan(y), np.isnan(ry))
+                inf = np.isinf(ry)
+                np.testing.assert_array_equal(np.where(inf, y, 0), np.where(inf, ry, 0))
+                fin = np.isfinite(ry)
+                assert_close(np.where(fin, y, 0), np.where(fin, ry, 0), 2 * 128, f"step {step}")
+    finally:
+        pywelvet.set_tuning("sgd_batch", old)
+
+
 @pytest.mark.parametrize("dtype", [9, 13, 14], ids=["int8", "uint8", "int4"])
 def test_batched_sgd_bad_last_store_updates_the_earlier_ones(oracle, dtype):
     """One SGD launch for two stores of one dtype where only the second

@@ -313,13 +313,23 @@ __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ bod
 // code load, four float4 gradient loads and 16-byte stores (of the
 // decode-ready copy too, for FP8); the first block's threads take the
 // n mod 16 tail.  The per-element arithmetic is sgd_kernel's.
+// E5M2 (nf non-null): *nf |= 1 when a new decode-ready code has the all-ones
+// exponent (Inf or NaN), so the store's finiteness is known after the step.
 template <int DT, int G>
 __device__ inline void sgd8_units(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
                                   const float *__restrict__ g, double lr, float scale, float minv,
-                                  int64_t blk, int64_t nblk) {
+                                  int64_t blk, int64_t nblk, int *nf = nullptr) {
   static_assert(dtype_bits(DT) == 8 && fix_bytes<DT>() == 1, "one-byte codes");
   static_assert(G == 4 || G == 16, "elements per thread");
   constexpr int NWD = G / 4;  // code words per thread
+  constexpr bool kTrack = DT == kFP8E5M2;
+  // a byte of w is an E5M2 Inf / NaN code: (b & 0x7c) == 0x7c, i.e. a zero
+  // byte in (w & 0x7c7c7c7c) ^ 0x7c7c7c7c (whose bytes are below 0x80)
+  auto nonfinite4 = [](uint32_t w) {
+    const uint32_t v = (w & 0x7c7c7c7cu) ^ 0x7c7c7c7cu;
+    return ((v - 0x01010101u) & ~v & 0x80808080u) != 0;
+  };
+  bool bad = false;
   const int64_t groups = n / G;
   for (int64_t q = blk * kThreads + threadIdx.x; q < groups; q += nblk * kThreads) {
     const int64_t i0 = q * G;
@@ -353,12 +363,23 @@ __device__ inline void sgd8_units(uint8_t *__restrict__ body, uint8_t *__restric
       *(uint32_t *)(body + i0) = ow[0];
       if constexpr (has_kcopy<DT>()) *(uint32_t *)(kbody + i0) = kw[0];
     }
+    if constexpr (kTrack) {
+#pragma unroll
+      for (int v = 0; v < NWD; ++v) bad |= nonfinite4(kw[v]);
+    }
   }
   const int64_t i = groups * G + threadIdx.x;
   if (blk == 0 && i < n) {
     const uint32_t nc = (uint32_t)fix_code<DT>(sgd_value<DT>(body[i], i, g[i], lr, scale, minv), scale, minv) & 0xffu;
-    if constexpr (has_kcopy<DT>()) kbody[i] = kcode<DT>(nc);
+    if constexpr (has_kcopy<DT>()) {
+      const uint8_t k = kcode<DT>(nc);
+      kbody[i] = k;
+      if constexpr (kTrack) bad |= (k & 0x7cu) == 0x7cu;
+    }
     body[i] = (uint8_t)nc;
+  }
+  if constexpr (kTrack) {
+    if (nf != nullptr && __any(bad) && (threadIdx.x & 63) == 0) atomicOr(nf, 1);
   }
 }
 
@@ -366,9 +387,9 @@ template <int DT, int G>
 __global__ void __launch_bounds__(kThreads) sgd8_kernel(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody,
                                                         int64_t n, const float *__restrict__ g, double lr,
                                                         float scale, float minv, int *stop, const int *bad,
-                                                        int bad_value) {
+                                                        int bad_value, int *nf) {
   if (sgd_stopped(stop, bad, bad_value)) return;
-  sgd8_units<DT, G>(body, kbody, n, g, lr, scale, minv, blockIdx.x, gridDim.x);
+  sgd8_units<DT, G>(body, kbody, n, g, lr, scale, minv, blockIdx.x, gridDim.x, nf);
 }
 
 // Float64 storage keeps full f64: w = w - lr*g (native_codec.cpp:933-939
@@ -432,7 +453,7 @@ __global__ void __launch_bounds__(kThreads) sgd_batch_kernel(SgdBatch b, double 
   if constexpr (DT == kFloat32) sgd_f32_units((float *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
   else if constexpr (DT == kFloat64) sgd_f64_units((double *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
   else if constexpr (dtype_bits(DT) == 8 && fix_bytes<DT>() == 1)
-    sgd8_units<DT, G>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x);
+    sgd8_units<DT, G>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x, t.nonfinite);
   else
     sgd_units<DT>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x);
 }
@@ -519,7 +540,8 @@ hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s
 }
 
 hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
-                      float scale, float minv, int *stop, const int *bad, int bad_value, hipStream_t s) {
+                      float scale, float minv, int *stop, const int *bad, int bad_value, hipStream_t s,
+                      int *nonfinite) {
   if ((dt == kFP8E4M3 || dt == kFP8E5M2) && kbody == nullptr) return hipErrorInvalidValue;
   if (dt == kFloat32) {
     sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop, bad, bad_value);
@@ -533,10 +555,10 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
   if constexpr (dtype_bits(D) == 8 && fix_bytes<D>() == 1) {                               \
     if (n >= ((int64_t)4 << 20))                                                            \
       sgd8_kernel<D, 16><<<grid_for(n / 16 + 1), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, \
-                                                                  stop, bad, bad_value);    \
+                                                                  stop, bad, bad_value, nonfinite); \
     else /* small stores: four codes per thread, four times the threads */                \
       sgd8_kernel<D, 4><<<grid_for(n / 4 + 1), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, \
-                                                                stop, bad, bad_value);      \
+                                                                stop, bad, bad_value, nonfinite); \
     return hipGetLastError();                                                               \
   } else if constexpr (D != kFloat32 && D != kFloat64) {                                    \
     sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \

@@ -4,25 +4,35 @@
 // (welvet_dense.metal:54-178): weights stay packed in HBM and are decoded in
 // registers (through LDS tables for formats of <= 8 bits) inside the product.
 //
-//   forward, batch <= 4   gemv_kernel: a 64-lane wave owns R rows, lanes
-//                         stream 16-byte chunks of each row (coalesced), x
-//                         chunks are reused across the R rows, DPP/shuffle
-//                         reduction, bias + activation fused in the store.
-//   forward, batch > 4    gemm_sk_kernel: decoded W tiles and x tiles staged in
-//                         LDS, fp32 MFMA 32x32x2, split-K with an ordered f64
-//                         reduction that applies bias + activation.
+//   forward, batch 1      gemv_pf_kernel / gemv_loop_kernel: lanes stream
+//                         16-byte chunks of a row (C per lane, all loads
+//                         issued before any decode), R rows per block, x in
+//                         registers; the loop form walks the row groups with a
+//                         fixed grid.  Bias + activation fused in the store.
+//   forward, batch 2-8    gemv_loopb_kernel where the batch's x fits in
+//                         registers; gemv_kernel for other batch <= 4 shapes.
+//   forward, batch > 4    split-x bf16 MFMA GEMM (x = three exact bf16 parts)
+//                         for FP8 / Int8 / FP4 / NF4: gemm_bf3r_kernel without
+//                         a k split, else gemm_bf3{,s,k}_kernel + sk_reduce;
+//                         fp32 MFMA gemm_regr / gemm_regx (batch <= 16, no k
+//                         split), gemm_reg / gemm_sk (+ sk_reduce) for the
+//                         other formats.
 //   dX, batch <= 2        dx_small_kernel: lanes own column chunks and walk a
-//                         segment of rows (coalesced), ordered f64 reduction
-//                         over segments.
-//   dX, batch > 2         gemm_sk_kernel with the transposed W tile loader.
-//   dW                    dw_kernel: VALU sequential fmaf over the batch in
-//                         batch order, bit-identical to the reference's
-//                         outer-product accumulation (welvet_dense.metal:155-178).
+//                         segment of rows (coalesced), ordered reduction.
+//   dX, batch > 2         gemm_regt_kernel (batch <= 16), the split-x GEMM over
+//                         the store's transposed copy, or gemm_sk through the
+//                         transposed tile loader; the next layer's activation
+//                         derivative fused in the store where it is piecewise.
+//   dW                    dw_mfma_kernel / dw_batch_kernel: fp32 MFMA over the
+//                         batch with the reference's per-element rounding
+//                         (welvet_dense.metal:155-178).
+//   unaligned rows        gemv_generic_kernel / dx_generic_kernel.
 //
 // Accumulation is fp32 inside a lane/tile and f64 across split-K / segment
 // partials; outputs are fl32 of that, within the stated tolerance of the f64
 // contract.  Float64 storage accumulates in f64 on the GEMV path.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "codec.hpp"
@@ -383,84 +393,6 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
                          (int64_t)b * a.N + row);
       }
     }
-  }
-}
-
-// Batch-1 GEMV, column-stationary: the block's G waves split the row into
-// 64-chunk column groups (lane = one chunk, x chunk held in registers for the
-// whole kernel) and stream the block's rows in batches of 8 with all eight
-// chunk loads in flight.  Per row batch each lane forms 8 partial dots
-// (fp32 FMA over one chunk, or f64 when ACC64), a butterfly transpose-reduce
-// leaves lane l with the 64-lane sum of row (l >> 3) in f64, and the waves'
-// partials are added in wave order.
-constexpr int kRB = 8;
-
-template <int F, bool ACC64>
-__global__ void __launch_bounds__(1024) gemv1_kernel(GemvArgs a, int rows_per_block) {
-  using I = FI<F>;
-  using Acc = std::conditional_t<ACC64 || F == FF64, double, float>;
-  constexpr int E = I::kE, W = I::kW;
-  __shared__ float lut_s[I::kTable];
-  __shared__ double part[16][kRB];
-  if constexpr (I::kLut) fill_table<F>(lut_s, a.lut, threadIdx.x, blockDim.x);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, G = blockDim.x >> 6;
-  const int c = wave * 64 + lane;
-  const bool active = c < a.nchunks;
-  Acc xv[E];
-  {
-    float xf[E];
-    if (active) load_x<E>(a.x + (int64_t)c * E, xf);
-#pragma unroll
-    for (int e = 0; e < E; ++e) xv[e] = active ? (Acc)xf[e] : (Acc)0;
-  }
-  __syncthreads();
-  const int r_begin = blockIdx.x * rows_per_block;
-  const int r_end = min(a.N, r_begin + rows_per_block);
-  const uint8_t *base = a.body + (int64_t)c * (W * 4);
-  for (int r0 = r_begin; r0 < r_end; r0 += kRB) {
-    uint32_t w[kRB][W];
-#pragma unroll
-    for (int r = 0; r < kRB; ++r) {
-      if (active && r0 + r < r_end) load_words<W>(base + (int64_t)(r0 + r) * a.row_bytes, w[r]);
-      else {
-#pragma unroll
-        for (int i = 0; i < W; ++i) w[r][i] = 0;
-      }
-    }
-    double acc[kRB];
-#pragma unroll
-    for (int r = 0; r < kRB; ++r) {
-      Acc s = 0;
-#pragma unroll
-      for (int e = 0; e < E; ++e) s = fma((Acc)chunk_value<F>(w[r], e, lut_s, a.scale, a.minv), xv[e], s);
-      acc[r] = active ? (double)s : 0.0;  // inactive lanes decode zero words: keep them out
-    }
-    // butterfly: after the xor-32/16/8 steps lane l holds row (l >> 3)
-    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1, b3 = (lane >> 3) & 1;
-    double t4[4], t2[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const double keep = b5 ? acc[i + 4] : acc[i], send = b5 ? acc[i] : acc[i + 4];
-      t4[i] = keep + __shfl_xor(send, 32);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const double keep = b4 ? t4[i + 2] : t4[i], send = b4 ? t4[i] : t4[i + 2];
-      t2[i] = keep + __shfl_xor(send, 16);
-    }
-    double v = (b3 ? t2[1] : t2[0]) + __shfl_xor(b3 ? t2[0] : t2[1], 8);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 1);
-    if ((lane & 7) == 0) part[wave][lane >> 3] = v;
-    __syncthreads();
-    if (threadIdx.x < kRB && r0 + (int)threadIdx.x < r_end) {
-      double s = 0;
-      for (int g = 0; g < G; ++g) s += part[g][threadIdx.x];
-      const int row = r0 + threadIdx.x;
-      bias_act_store(s, row, a.bias, a.bias_len, a.act, a.pre, a.post, row);
-    }
-    __syncthreads();
   }
 }
 
@@ -2705,53 +2637,6 @@ __global__ void __launch_bounds__(256) dx_generic_kernel(DevStore w, int batch, 
   }
 }
 
-// dW[o][i] = sequential fmaf over b (welvet_dense.metal:155-178).
-__global__ void __launch_bounds__(256) dw_kernel(const float *__restrict__ dpre,
-                                                 const float *__restrict__ x, int B, int rows, int cols,
-                                                 float *__restrict__ dW, int *flag) {
-  __shared__ float Ds[32][64];
-  __shared__ float Xs[32][64];
-  const int tid = threadIdx.x, to = tid >> 4, ti = tid & 15;
-  const int o0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
-  float acc[4][4] = {};
-  for (int b0 = 0; b0 < B; b0 += 32) {
-    __syncthreads();
-    for (int q = tid; q < 32 * 64; q += 256) {
-      const int bb = q >> 6, j = q & 63, b = b0 + bb;
-      Ds[bb][j] = (b < B && o0 + j < rows) ? dpre[(int64_t)b * rows + o0 + j] : 0.0f;
-      Xs[bb][j] = (b < B && i0 + j < cols) ? x[(int64_t)b * cols + i0 + j] : 0.0f;
-    }
-    __syncthreads();
-    const int nb = min(32, B - b0);
-    for (int bb = 0; bb < nb; ++bb) {
-      float d[4], xv[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) d[r] = Ds[bb][to * 4 + r];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) xv[c] = Xs[bb][ti * 4 + c];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(d[r], xv[c], acc[r][c]);
-    }
-  }
-  int bad = 0;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int o = o0 + to * 4 + r;
-    if (o >= rows) continue;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int i = i0 + ti * 4 + c;
-      if (i < cols) {
-        dW[(int64_t)o * cols + i] = acc[r][c];
-        bad |= !isfinite(acc[r][c]);
-      }
-    }
-  }
-  if (flag != nullptr && __any(bad) && (tid & 63) == 0) atomicOr(flag, 1);
-}
-
 // dW on the matrix cores with the reference's rounding.  Per output the
 // reference accumulates acc = fmaf(dpre[b][o], x[b][i], acc) over b in batch
 // order from 0 (welvet_dense.metal:155-178).  v_mfma_f32_32x32x2f32 computes
@@ -3060,7 +2945,13 @@ __global__ void __launch_bounds__(256) add_kernel(const float *__restrict__ a,
 // --------------------------------------------------------------- dispatch
 int g_forward_path = 0;
 // Tuning knobs (welvet_hip_set_tuning); defaults are the measured choices.
-int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1, 1, 1, 1};
+// Route switches (welvet_hip_set_tuning; kept keys only, the others are
+// unknown): read by every launch, written by any thread, hence atomic.
+std::atomic<int> g_tune[kNumTune] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1};
+bool tune_key_kept(int key) {
+  return key == kTuneBf3 || (key >= kTuneBf3Rows && key <= kTuneRegx);
+}
+inline int knob(int key) { return g_tune[key].load(std::memory_order_relaxed); }
 
 // Kind of a dtype under the current knobs, -1 when the split-x GEMM does not
 // take it.
@@ -3069,9 +2960,9 @@ int g_tune[kNumTune] = {1, 0, 0, 0, 1, 0, 1, 1, 0, -1, 1, 0, 0, 2, 1, 1, 1, 1, 1
 // parts of x would give NaN where the fp32 product is Inf.
 int bf3_kind(const DevStore &w) {
   const int dt = w.dtype;
-  if (g_tune[kTuneBf3] == 0) return -1;
-  if (dt == kFP8E4M3 && g_tune[kTuneFastDecode] != 0) return BK_E4;
-  if (dt == kFP8E5M2 && g_tune[kTuneFastDecode] != 0 && w.finite) return BK_E5;
+  if (knob(kTuneBf3) == 0) return -1;
+  if (dt == kFP8E4M3) return BK_E4;
+  if (dt == kFP8E5M2 && w.finite) return BK_E5;
   if (dt == kInt8) return BK_I8;
   if (dt == kFP4) return BK_FP4;
   if (dt == kNF4) return BK_NF4;
@@ -3088,30 +2979,22 @@ bool chunk_aligned(const DevStore &w, int64_t len) {
   return f >= 0 && len % fmt_chunk_elems(f) == 0;
 }
 
-// Formats whose batch-1 GEMV takes the rows-per-block knob.
-constexpr bool gemv_rows_knob(int f) {
-  return f == FE4 || f == FE5 || f == FI8 || f == FL4P || f == FL4 || f == FL8 || f == FH16 ||
-         f == FB16 || f == FF4;
+// Formats whose batch-1 GEMV also has the (1, 4) and (2, 8) shapes of
+// (chunks per lane, rows per block) besides the default (C, 8 / C).
+constexpr bool gemv_extra_rows(int f) {
+  return f == FE4 || f == FE5 || f == FI8 || f == FL4P || f == FF4;
 }
 
-// (chunks per lane, rows per block) shapes of the all-loads GEMV built in
-// addition to the default (C, 8 / C).
-constexpr bool gemv_pf_extra(int C, int R) {
-  return (C == 1 && (R == 1 || R == 2 || R == 4 || R == 16)) ||
-         (C == 2 && (R == 1 || R == 2 || R == 8)) || (C == 4 && R == 1);
-}
-
-// Kernel format of a dtype under the current knobs.
+// Kernel format of a dtype: FP8 and FP4 through the hardware converters
+// (FP8 from the decode-ready copy), Int8 by integer conversion, the other
+// 4-bit formats through the byte-pair table, the rest as fmt_of.
 int kernel_fmt(int dt) {
+  if (dt == kFP8E4M3) return FE4;
+  if (dt == kFP8E5M2) return FE5;
+  if (dt == kInt8) return FI8;
+  if (dt == kFP4) return FF4;
   const int f = fmt_of(dt);
-  if (g_tune[kTuneFastDecode]) {
-    if (dt == kFP8E4M3) return FE4;
-    if (dt == kFP8E5M2) return FE5;
-    if (dt == kInt8) return FI8;
-    if (dt == kFP4) return FF4;
-  }
-  if (f == FL4 && g_tune[kTunePairLut]) return FL4P;
-  return f;
+  return f == FL4 ? FL4P : f;
 }
 
 // Payload a kernel format reads: the decode-ready copy for the formats
@@ -3173,8 +3056,8 @@ bool reg_gemm_ok(int f) { return f >= 0 && fmt_chunk_elems(f) >= 8; }  // format
 // register-B kernel for other <= 16-bit formats, else the LDS-staged kernel.
 SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
   if (bk >= 0) {
-    const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
-    const int bm = (M <= 16 && g_tune[kTuneBf3Small] != 0) ? 16 : M <= 32 ? 32 : 64;
+    const int occ = 2;
+    const int bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
     // tile width: 128 output columns where outputs are few (N <= 8192) for
     // the 16-row tile and for the one-byte kinds' 32-row tile (their
     // stream-K partial tiles then weigh as much as the weights: 4096^2 FP8
@@ -3182,15 +3065,13 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     // 17.2; 11008 -> 4096 FP8 b16 21.4 against 22.9), else 256 (4096 ->
     // 11008 b8 FP8 19.6 against 20.1; the 4-bit kinds' 32-row tile keeps
     // the two-group workgroups, which need 256)
-    const int ck = g_tune[kTuneBf3Cols];
-    const bool narrow = ck == 1 || (ck == 0 && N <= 8192 &&
-                                    (bm == 16 || (bm == 32 && bk != BK_NF4 && bk != BK_FP4)));
+    const bool narrow = N <= 8192 && (bm == 16 || (bm == 32 && bk != BK_NF4 && bk != BK_FP4));
     const int bn = narrow ? 128 : 256;
     const int stages = (K + kBK - 1) / kBK;
     // no k split for K <= 2048 (measured at batch 5-16: 1024^2 6.6 against
     // 10.3 us, 2048 -> 4096 9.4 against 14.3; at K = 4096 about even, at
     // K = 11008 1.6x slower: too few workgroups for the serial K walk)
-    const int rk = g_tune[kTuneBf3Rows];
+    const int rk = knob(kTuneBf3Rows);
     if (bm == 16 && K % 8 == 0 && (rk == 2 || (rk == 1 && K <= 2048))) {
       SkPlan p;
       p.bf3 = p.rows = true;
@@ -3207,9 +3088,9 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     }
     // two-group workgroups: every 64-row tile; 32-row tiles only for the
     // 4-bit kinds (FP8 / Int8 measured slower there)
-    const bool groups = g_tune[kTuneBf3Groups] != 0 && bn == 256 && stages % 2 == 0 &&
+    const bool groups = bn == 256 && stages % 2 == 0 &&
                         (bm == 64 || (bm == 32 && (bk == BK_NF4 || bk == BK_FP4)));
-    SkPlan p = groups ? plan_sk(M, K, N, bm, bn, g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 1, 2)
+    SkPlan p = groups ? plan_sk(M, K, N, bm, bn, 1, 2)
                       : plan_sk(M, K, N, bm, bn, occ);
     p.bf3 = true;
     return p;
@@ -3225,7 +3106,7 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
   // 3-bit tables 29-30 / 38-40 against 42 / 42, Int64 82 / 86 against 110 /
   // 112, Complex128 167 / 177 against 190 / 183; Uint8, Uint16, FP6, Int5
   // and Complex64 lose at b16)
-  const int rk = g_tune[kTuneBf3Rows];
+  const int rk = knob(kTuneBf3Rows);
   const bool half = f == FH16 || f == FB16, int16 = f == FI16 || f == FU16;
   const bool wide_ok = f == FI32 || f == FU32 || f == FI64 || f == FU64 || f == FL1 || f == FL2 ||
                        f == FL3 || f == FC128;
@@ -3244,10 +3125,7 @@ SkPlan plan_fwd_gemm(int f, int bk, int M, int K, int N) {
     p.ws_bytes = 0;
     return p;
   }
-  if (reg_gemm_ok(f) && g_tune[kTuneRegGemm] != 0) {
-    const int occ = g_tune[kTuneGemmOcc] > 0 ? g_tune[kTuneGemmOcc] : 2;
-    return plan_sk(M, K, N, M <= 32 ? 32 : 64, kRegBN, occ);
-  }
+  if (reg_gemm_ok(f)) return plan_sk(M, K, N, M <= 32 ? 32 : 64, kRegBN, 2);
   return plan_sk(M, K, N);
 }
 
@@ -3268,7 +3146,7 @@ constexpr bool gemv_batch_fmt(int f) {
          f == FU64 || f == FL1 || f == FL2 || f == FL3 || f == FL5 || f == FL6;
 }
 bool gemv_batch_shape(int f, int batch, int nchunks, int rows, GemvBatchShape &sh) {
-  if (g_tune[kTuneGemvBatch] == 0 || batch < 2 || batch > 8 || nchunks < 1 || rows < 1) return false;
+  if (knob(kTuneGemvBatch) == 0 || batch < 2 || batch > 8 || nchunks < 1 || rows < 1) return false;
   if (!gemv_batch_fmt(f)) return false;
   const int E = fmt_chunk_elems(f);
   const int B = batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
@@ -3333,7 +3211,7 @@ hipError_t gemv_dispatch(int batch, const GemvArgs &a, hipStream_t s) {
 
 #define WH_FMT_SWITCH(f, F)                                                                          \
   switch (f) {                                                                                       \
-  case FL1: F(FL1); case FL2: F(FL2); case FL3: F(FL3); case FL4: F(FL4); case FL5: F(FL5);          \
+  case FL1: F(FL1); case FL2: F(FL2); case FL3: F(FL3); case FL5: F(FL5);                            \
   case FL6: F(FL6); case FL8: F(FL8); case FH16: F(FH16); case FB16: F(FB16); case FI16: F(FI16);    \
   case FU16: F(FU16); case FF32: F(FF32); case FI32: F(FI32); case FU32: F(FU32); case FI64: F(FI64); \
   case FU64: F(FU64); case FC64: F(FC64); case FC128: F(FC128); case FF64: F(FF64);                  \
@@ -3361,13 +3239,11 @@ hipError_t gemv_dispatch(int batch, const GemvArgs &a, hipStream_t s) {
 void set_forward_path(int path) { g_forward_path = path; }
 
 int set_tuning(int key, int value) {
-  if (key < 0 || key >= kNumTune) return -1;
-  const int old = g_tune[key];
-  g_tune[key] = value;
-  return old;
+  if (key < 0 || key >= kNumTune || !tune_key_kept(key)) return -1;
+  return g_tune[key].exchange(value, std::memory_order_relaxed);
 }
 
-int tuning(int key) { return key < 0 || key >= kNumTune ? -1 : g_tune[key]; }
+int tuning(int key) { return key < 0 || key >= kNumTune || !tune_key_kept(key) ? -1 : knob(key); }
 
 size_t forward_workspace_bytes(const DevStore &w, int batch) {
   if (fwd_route(w, batch) != 2) return 0;
@@ -3380,10 +3256,7 @@ template <bool FWD>
 hipError_t launch_bf3r(const SkPlan &p, int bk, const GemmArgs &a, const double *bias, int bias_len,
                        int act, float *out, float *post, hipStream_t s) {
   const dim3 grid(p.gx, p.gy);
-  const bool d2 = g_tune[kTuneBf3Depth] == 2;
-#define WH_GR3(BK)                                                                                  \
-  if (d2) gemm_bf3r_kernel<BK, 2, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);      \
-  else gemm_bf3r_kernel<BK, 4, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);
+#define WH_GR3(BK) gemm_bf3r_kernel<BK, 4, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);
   switch (bk) {
   case BK_E4: WH_GR3(BK_E4) break;
   case BK_I8: WH_GR3(BK_I8) break;
@@ -3398,33 +3271,22 @@ hipError_t launch_bf3r(const SkPlan &p, int bk, const GemmArgs &a, const double 
 
 // The split-x GEMM of plan p for weight kind bk (a.body, a.post set).
 hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
-  const int dep = g_tune[kTuneBf3Depth];
-#define WH_GB(BK, D1)                                                                 \
+#define WH_GB(BK)                                                                     \
   if (p.bm == 16) {                                                                   \
-    if (p.bn == 128) gemm_bf3s_kernel<BK, D1, 1><<<p.blocks, 256, 0, s>>>(a);          \
-    else if (dep >= 3) gemm_bf3s_kernel<BK, 4, 2><<<p.blocks, 256, 0, s>>>(a);         \
-    else if (dep == 2 || D1 == 2) gemm_bf3s_kernel<BK, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    if (p.bn == 128) gemm_bf3s_kernel<BK, 1, 1><<<p.blocks, 256, 0, s>>>(a);           \
     else gemm_bf3s_kernel<BK, 1, 2><<<p.blocks, 256, 0, s>>>(a);                       \
   } else if (p.bm == 32) {                                                            \
-    if (p.bn == 128) gemm_bf3_kernel<BK, 1, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
-    else if (dep == 3) gemm_bf3_kernel<BK, 1, 3, 2><<<p.blocks, 256, 0, s>>>(a);       \
-    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 1, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    if (p.bn == 128) gemm_bf3_kernel<BK, 1, 1, 1><<<p.blocks, 256, 0, s>>>(a);         \
     else gemm_bf3_kernel<BK, 1, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
   } else {                                                                            \
-    if (p.bn == 128) gemm_bf3_kernel<BK, 2, D1, 1><<<p.blocks, 256, 0, s>>>(a);        \
-    else if (dep == 2 || D1 == 2) gemm_bf3_kernel<BK, 2, 2, 2><<<p.blocks, 256, 0, s>>>(a); \
+    if (p.bn == 128) gemm_bf3_kernel<BK, 2, 1, 1><<<p.blocks, 256, 0, s>>>(a);         \
     else gemm_bf3_kernel<BK, 2, 1, 2><<<p.blocks, 256, 0, s>>>(a);                     \
   }
   if (p.rows) return hipErrorInvalidValue;  // launched with its epilogue by the caller
-  if (p.kg == 2) {  // ring depth 2 unless the knob asks for 1
+  if (p.kg == 2) {  // two wave groups, a ring two units deep
 #define WH_GK(BK)                                                                             \
-  if (p.bm == 32) {                                                                           \
-    if (dep == 1) gemm_bf3k_kernel<BK, 1, 1, 2><<<p.blocks, 512, 0, s>>>(a);                  \
-    else gemm_bf3k_kernel<BK, 1, 2, 2><<<p.blocks, 512, 0, s>>>(a);                           \
-  } else {                                                                                    \
-    if (dep == 1) gemm_bf3k_kernel<BK, 2, 1, 2><<<p.blocks, 512, 0, s>>>(a);                  \
-    else gemm_bf3k_kernel<BK, 2, 2, 2><<<p.blocks, 512, 0, s>>>(a);                           \
-  }
+  if (p.bm == 32) gemm_bf3k_kernel<BK, 1, 2, 2><<<p.blocks, 512, 0, s>>>(a);                  \
+  else gemm_bf3k_kernel<BK, 2, 2, 2><<<p.blocks, 512, 0, s>>>(a);
     switch (bk) {
     case BK_E4: WH_GK(BK_E4) break;
     case BK_I8: WH_GK(BK_I8) break;
@@ -3437,11 +3299,11 @@ hipError_t launch_bf3(const SkPlan &p, int bk, GemmArgs &a, hipStream_t s) {
     return hipGetLastError();
   }
   switch (bk) {
-  case BK_E4: WH_GB(BK_E4, 1) break;
-  case BK_I8: WH_GB(BK_I8, 1) break;
-  case BK_FP4: WH_GB(BK_FP4, 1) break;
-  case BK_NF4: WH_GB(BK_NF4, 1) break;
-  case BK_E5: WH_GB(BK_E5, 1) break;
+  case BK_E4: WH_GB(BK_E4) break;
+  case BK_I8: WH_GB(BK_I8) break;
+  case BK_FP4: WH_GB(BK_FP4) break;
+  case BK_NF4: WH_GB(BK_NF4) break;
+  case BK_E5: WH_GB(BK_E5) break;
   default: return hipErrorInvalidValue;
   }
 #undef WH_GB
@@ -3491,7 +3353,7 @@ template <int F, int C, int R, int B>
 hipError_t launch_loopb(const GemvArgs &a, int batch, int S, hipStream_t s) {
   const int ngroups = (a.N + R - 1) / R;
   const int threads = 64 * S;
-  const int k = g_tune[kTuneGemvBatch];
+  const int k = knob(kTuneGemvBatch);
   int blocks;
   if (k >= 2) {
     blocks = k * num_cus() / S;
@@ -3567,122 +3429,83 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   if (route == 1) {
     GemvArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, x, w.cols, w.rows, w.cols / fmt_chunk_elems(f),
                row_bytes_of(w), bias, bias_len, act, pre, post};
-    if (batch == 1 && g_tune[kTuneGemv1] == 1) {
-      // (C, R): chunks per lane and rows per block.  Auto: the fewest chunks
-      // per lane that cover a row with at most 4 waves, and 8 / C rows; for
-      // FP8 / Int8 rows of one chunk per lane and for 4-bit rows that two
-      // chunks per lane cover, 4 rows (measured best: more blocks in flight
-      // for the heavier FP8 decode, one wave per block for 4-bit)
-      int C = 1, Rauto = 0;
-      int auto_wpc = -1;  // -1: the format's default grid
-      switch (g_tune[kTuneCR]) {
-      case 1: C = 2; break;
-      case 2: C = 4; break;
-      case 3: C = 1; break;
-      case 4: C = 8; break;
-      default:
-        while (C < 8 && (a.nchunks + 64 * C - 1) / (64 * C) > 4) C *= 2;
-        if ((f == FE4 || f == FE5 || f == FI8) && C == 1) Rauto = 4;
-        if (f == FF4 && C == 1) Rauto = 8;
-        if ((f == FL4P || f == FL4) && a.nchunks <= 128) C = 2, Rauto = 4;
-        // pair-table rows of at most two waves of one chunk per lane, with
-        // more 4-row groups than 16 waves per CU hold: one chunk per lane in
-        // the fixed-grid loop (measured at 4096 -> 11008: 8.90-8.96 against
-        // 9.22-9.30 us with two chunks per lane, one block per group)
-        if (f == FL4P && a.nchunks <= 128 &&
-            16 * num_cus() / ((a.nchunks + 63) / 64) < (a.N + 3) / 4)
-          C = 1, Rauto = 4, auto_wpc = 16;
-        // rows of 5-8 waves of one chunk per lane (8224-16384 inputs of a
-        // 4-bit format): NF4 one chunk per lane, 4 rows per group, the loop
-        // at 12 waves per CU (11008 -> 4096: 9.5 against 10.2 us); FP8 rows
-        // of 5-8 waves of two chunks per lane: two chunks per lane, 8 rows
-        // per block, one block per group (11008 -> 4096: 11.3 against
-        // 13.3-13.9 us with four chunks per lane)
-        {
-          const int s1 = (a.nchunks + 63) / 64, s2 = (a.nchunks + 127) / 128;
-          if (f == FL4P && s1 >= 5 && s1 <= 8) C = 1, Rauto = 4, auto_wpc = 12;
-          if ((f == FE4 || f == FE5) && s1 > 8 && s2 >= 5 && s2 <= 8) C = 2, Rauto = 8, auto_wpc = 0;
-        }
-        // 4-bit rows that take three or more waves of two chunks per lane
-        // (11008-wide inputs): 8 rows per block (measured at 11008 -> 4096:
-        // FP4 8.2 against 9.1 us, NF4 10.2 against 10.6 us with 4)
-        if ((f == FL4P || f == FL4 || f == FF4) && C == 2 && a.nchunks > 256) Rauto = 8;
+    if (batch == 1) {
+      // (C, R): chunks per lane and rows per block.  The fewest chunks per
+      // lane that cover a row with at most 4 waves, and 8 / C rows; for FP8 /
+      // Int8 rows of one chunk per lane and for 4-bit rows that two chunks
+      // per lane cover, 4 rows (measured best: more blocks in flight for the
+      // heavier FP8 decode, one wave per block for 4-bit).  wpc: waves per CU
+      // of a fixed grid walking the row groups (0 = one block per group, -1 =
+      // the format's default)
+      int C = 1, R = 0, wpc = -1;
+      while (C < 8 && (a.nchunks + 64 * C - 1) / (64 * C) > 4) C *= 2;
+      if ((f == FE4 || f == FE5 || f == FI8) && C == 1) R = 4;
+      if (f == FL4P && a.nchunks <= 128) C = 2, R = 4;
+      // pair-table rows of at most two waves of one chunk per lane, with
+      // more 4-row groups than 16 waves per CU hold: one chunk per lane in
+      // the fixed-grid loop (measured at 4096 -> 11008: 8.90-8.96 against
+      // 9.22-9.30 us with two chunks per lane, one block per group)
+      if (f == FL4P && a.nchunks <= 128 && 16 * num_cus() / ((a.nchunks + 63) / 64) < (a.N + 3) / 4)
+        C = 1, R = 4, wpc = 16;
+      // rows of 5-8 waves of one chunk per lane (8224-16384 inputs of a
+      // 4-bit format): NF4 one chunk per lane, 4 rows per group, the loop
+      // at 12 waves per CU (11008 -> 4096: 9.5 against 10.2 us); FP8 rows
+      // of 5-8 waves of two chunks per lane: two chunks per lane, 8 rows
+      // per block, one block per group (11008 -> 4096: 11.3 against
+      // 13.3-13.9 us with four chunks per lane)
+      {
+        const int s1 = (a.nchunks + 63) / 64, s2 = (a.nchunks + 127) / 128;
+        if (f == FL4P && s1 >= 5 && s1 <= 8) C = 1, R = 4, wpc = 12;
+        if ((f == FE4 || f == FE5) && s1 > 8 && s2 >= 5 && s2 <= 8) C = 2, R = 8, wpc = 0;
       }
+      // 4-bit rows that take three or more waves of two chunks per lane
+      // (11008-wide inputs): 8 rows per block (measured at 11008 -> 4096:
+      // FP4 8.2 against 9.1 us, NF4 10.2 against 10.6 us with 4)
+      if ((f == FL4P || f == FF4) && C == 2 && a.nchunks > 256) R = 8;
       const int S = (a.nchunks + 64 * C - 1) / (64 * C);
       if (S <= 8) {
-        // rows per block: 8 / C, or the knob's value (else the auto choice)
-        // where that (C, R) kernel exists (the formats the sweeps cover)
-        int R = 8 / C;
-        const int rk = g_tune[kTuneGemvRows] ? g_tune[kTuneGemvRows] : Rauto;
-        if (gemv_rows_knob(f) && gemv_pf_extra(C, rk)) R = rk;
-        // grid: one block per row group, or (knob / FP8 and FP4 default) a
-        // fixed number of waves per CU walking the row groups, x loaded once
-        // each (the hardware-converter formats; others take one block per
-        // group)
+        if (R == 0 || !gemv_extra_rows(f)) R = 8 / C;
+        // grid: one block per row group, or (FP8 and FP4 by default) a fixed
+        // number of waves per CU walking the row groups, x loaded once each
         const int ngroups = (a.N + R - 1) / R;
-        int wpc = g_tune[kTuneGemvWaves];
-        int blocks = ngroups;
-        if (wpc < -1) blocks = (ngroups - wpc - 1) / -wpc;  // -k: k row groups per block
-        else {
-          if (wpc < 0) {
-            wpc = auto_wpc >= 0 ? auto_wpc : (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
-            // FP8 rows whose 16-wave grid would hold every row group: 12
-            // waves per CU, so the grid walks them (4096^2 config-2 leg:
-            // 5.15 against 5.60 us for one block per group)
-            if ((f == FE4 || f == FE5) && auto_wpc < 0 && 16 * num_cus() / S >= ngroups &&
-                12 * num_cus() / S < ngroups)
-              wpc = 12;
-          }
-          if (wpc > 0) blocks = std::max(1, std::min(ngroups, wpc * num_cus() / S));
+        if (wpc < 0) {
+          wpc = (f == FE4 || f == FE5 || f == FF4) ? 16 : 0;
+          // FP8 rows whose 16-wave grid would hold every row group: 12
+          // waves per CU, so the grid walks them (4096^2 config-2 leg:
+          // 5.15 against 5.60 us for one block per group)
+          if ((f == FE4 || f == FE5) && 16 * num_cus() / S >= ngroups && 12 * num_cus() / S < ngroups)
+            wpc = 12;
         }
-#define WH_PF(F)                                                                         \
-  if constexpr (F == FE4 || F == FE5 || F == FF4 || F == FL4P) {                         \
-    if (blocks < ngroups) {                                                              \
-      if (C == 1 && R == 4) gemv_loop_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);  \
-      else if (C == 1 && R == 8) gemv_loop_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a); \
-      else if (C == 1 && R == 2) gemv_loop_kernel<F, 1, 2><<<blocks, 64 * S, 0, s>>>(a); \
-      else if (C == 2 && R == 4) gemv_loop_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a); \
-      else blocks = ngroups;                                                             \
-      if (blocks < ngroups) return hipGetLastError();                                    \
-    }                                                                                    \
-  }                                                                                      \
-  blocks = ngroups;                                                                      \
-  if constexpr (gemv_rows_knob(F)) {                                                     \
-    if (R != 8 / C) {                                                                    \
-      if (C == 1 && R == 1) gemv_pf_kernel<F, 1, 1><<<blocks, 64 * S, 0, s>>>(a);        \
-      else if (C == 1 && R == 2) gemv_pf_kernel<F, 1, 2><<<blocks, 64 * S, 0, s>>>(a);   \
-      else if (C == 1 && R == 4) gemv_pf_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);   \
-      else if (C == 1 && R == 16) gemv_pf_kernel<F, 1, 16><<<blocks, 64 * S, 0, s>>>(a); \
-      else if (C == 2 && R == 1) gemv_pf_kernel<F, 2, 1><<<blocks, 64 * S, 0, s>>>(a);   \
-      else if (C == 2 && R == 2) gemv_pf_kernel<F, 2, 2><<<blocks, 64 * S, 0, s>>>(a);   \
-      else if (C == 2 && R == 8) gemv_pf_kernel<F, 2, 8><<<blocks, 64 * S, 0, s>>>(a);   \
-      else if (C == 4 && R == 1) gemv_pf_kernel<F, 4, 1><<<blocks, 64 * S, 0, s>>>(a);   \
-      else return hipErrorInvalidValue;                                                  \
-      return hipGetLastError();                                                          \
-    }                                                                                    \
-  }                                                                                      \
-  if (C == 1) gemv_pf_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a);                      \
-  else if (C == 2) gemv_pf_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a);                 \
-  else if (C == 4) gemv_pf_kernel<F, 4, 2><<<blocks, 64 * S, 0, s>>>(a);                 \
-  else gemv_pf_kernel<F, 8, 1><<<blocks, 64 * S, 0, s>>>(a);                             \
+        const int blocks = wpc > 0 ? std::max(1, std::min(ngroups, wpc * num_cus() / S)) : ngroups;
+#define WH_PF(F)                                                                          \
+  if constexpr (F == FE4 || F == FE5 || F == FF4 || F == FL4P) {                          \
+    /* the loop's shapes; any other takes one block per row group */                     \
+    const bool loop = blocks < ngroups && ((C == 1 && (R == 4 || R == 8)) || (C == 2 && R == 4)); \
+    if (loop) {                                                                           \
+      if (C == 1 && R == 4) gemv_loop_kernel<F, 1, 4><<<blocks, 64 * S, 0, s>>>(a);       \
+      else if (C == 1) gemv_loop_kernel<F, 1, 8><<<blocks, 64 * S, 0, s>>>(a);            \
+      else gemv_loop_kernel<F, 2, 4><<<blocks, 64 * S, 0, s>>>(a);                        \
+      return hipGetLastError();                                                           \
+    }                                                                                     \
+  }                                                                                       \
+  if constexpr (gemv_extra_rows(F)) {                                                     \
+    if (C == 1 && R == 4) {                                                               \
+      gemv_pf_kernel<F, 1, 4><<<ngroups, 64 * S, 0, s>>>(a);                              \
+      return hipGetLastError();                                                           \
+    }                                                                                     \
+    if (C == 2 && R == 8) {                                                               \
+      gemv_pf_kernel<F, 2, 8><<<ngroups, 64 * S, 0, s>>>(a);                              \
+      return hipGetLastError();                                                           \
+    }                                                                                     \
+  }                                                                                       \
+  if (C == 1) gemv_pf_kernel<F, 1, 8><<<ngroups, 64 * S, 0, s>>>(a);                      \
+  else if (C == 2) gemv_pf_kernel<F, 2, 4><<<ngroups, 64 * S, 0, s>>>(a);                 \
+  else if (C == 4) gemv_pf_kernel<F, 4, 2><<<ngroups, 64 * S, 0, s>>>(a);                 \
+  else gemv_pf_kernel<F, 8, 1><<<ngroups, 64 * S, 0, s>>>(a);                             \
   return hipGetLastError();
         WH_FMT_SWITCH(f, WH_PF)
 #undef WH_PF
       }
-    }
-    if (batch == 1 && a.nchunks <= 1024 && g_tune[kTuneGemv1] == 2) {
-      const int G = (a.nchunks + 63) / 64;
-      int rpb = g_tune[kTuneRowsPerBlock];
-      if (rpb <= 0) rpb = 16;
-      rpb = (rpb + kRB - 1) / kRB * kRB;
-      const int blocks = (a.N + rpb - 1) / rpb;
-      const bool acc64 = g_tune[kTuneAcc64] != 0;
-#define WH_GV1(F)                                                                   \
-  if (acc64) gemv1_kernel<F, true><<<blocks, 64 * G, 0, s>>>(a, rpb);               \
-  else gemv1_kernel<F, false><<<blocks, 64 * G, 0, s>>>(a, rpb);                    \
-  return hipGetLastError();
-      WH_FMT_SWITCH(f, WH_GV1)
-#undef WH_GV1
     }
     if (batched) {
       GemvBatchShape sh;
@@ -3728,7 +3551,7 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
     if (e != hipSuccess) return e;
   } else if (p.rows) {
 #define WH_GRR(F)                                                                                     \
-  if (batch <= 16 && w.cols <= kRegxMaxK && g_tune[kTuneRegx] != 0)                                   \
+  if (batch <= 16 && w.cols <= kRegxMaxK && knob(kTuneRegx) != 0)                                   \
     return launch_regx<F>(p, a, bias, bias_len, act, pre, post, s);                                   \
   gemm_regr_kernel<F, 8><<<dim3(p.gx, p.gy), 512, 0, s>>>(a, bias, bias_len, act, pre, post);          \
   break;
@@ -3786,7 +3609,7 @@ bool backward_wants_transposed(const DevStore &w, int batch) { return dx_bf3_kin
 // 270, Uint8 201 against 186, Float16 272 against 263; FP8 and Int8, whose
 // dX runs the split-x GEMM over their transposed codes, equal).
 bool dx_rows(const DevStore &w, int batch) {
-  const int rk = g_tune[kTuneBf3Rows];
+  const int rk = knob(kTuneBf3Rows);
   if (dx_route(w, batch) != 2 || batch > 16 || w.rows % 4 != 0) return false;
   if (rk == 2) return true;
   if (rk != 1) return false;
@@ -3816,7 +3639,7 @@ size_t backward_workspace_bytes(const DevStore &w, int batch) {
 }
 
 bool dw_batchable(const DevStore &w) {
-  return g_tune[kTuneDwMfma] == 2 && w.rows % 128 == 0 && w.cols % 128 == 0;
+  return w.rows % 128 == 0 && w.cols % 128 == 0;
 }
 
 // Deferring a layer's dW into a batched launch pays where the layer alone
@@ -3847,7 +3670,7 @@ hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s) {
 // no-split gemm_regt_kernel and the reduction of the stream-K GEMMs
 // (sk_reduce_kernel); not the transposed no-split bf3r epilogue.
 bool backward_dx_applies_next(const DevStore &w, int batch, int next_act) {
-  if (g_tune[kTuneFoldDeriv] == 0 || !act_piecewise(next_act)) return false;
+  if (knob(kTuneFoldDeriv) == 0 || !act_piecewise(next_act)) return false;
   if (dx_rows(w, batch)) return true;
   if (dx_route(w, batch) != 2) return false;
   const int bk = dx_bf3_kind(w, batch);
@@ -3917,7 +3740,7 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
     GemmArgs a{kernel_body(w, f), w.lut, w.scale, w.minv, dpre, batch, w.rows, w.cols, row_bytes_of(w),
                (w.cols + 15) / 16, (batch + 15) / 16, (w.rows + st - 1) / st, 0, 1, nullptr, 16, 16};
 #define WH_DXR(F)                                                                                   \
-  if (batch <= 16 && w.rows <= kRegtxMaxK && g_tune[kTuneRegx] != 0) {                              \
+  if (batch <= 16 && w.rows <= kRegtxMaxK && knob(kTuneRegx) != 0) {                              \
     e = launch_regtx<F>(a, dX, chain.dx_next_pre, chain.dx_next_act, s);                            \
     if (e != hipSuccess) return e;                                                                  \
     break;                                                                                          \
@@ -3954,12 +3777,9 @@ hipError_t launch_backward(const DevStore &w, int batch, const float *x, const f
   if (dw_batchable(w)) {
     dim3 g2(w.cols / 128, w.rows / 128);
     dw_mfma_lds_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
-  } else if (g_tune[kTuneDwMfma]) {
+  } else {
     dim3 g2((w.cols + 127) / 128, (w.rows + 127) / 128);
     dw_mfma_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
-  } else {
-    dim3 g2((w.cols + 63) / 64, (w.rows + 63) / 64);
-    dw_kernel<<<g2, 256, 0, s>>>(dpre, x, batch, w.rows, w.cols, dW, flag);
   }
   return hipGetLastError();
 }

@@ -51,10 +51,12 @@ hipError_t launch_lut(int dt, float scale, float minv, float *lut, hipStream_t s
 // SGD with fixed-scale re-encode; a no-op when `stop` is non-null and
 // *stop != 0, or when `bad` is non-null and *bad != 0 (a non-finite gradient
 // found upstream; then *stop = bad_value if it was 0).  FP8 formats also
-// refresh the decode-ready copy kbody (required for them).
+// refresh the decode-ready copy kbody (required for them).  E5M2 with
+// `nonfinite` non-null: *nonfinite |= 1 when a new code decodes to Inf or NaN
+// (the caller zeroes it first).
 hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const float *g, double lr,
                       float scale, float minv, int *stop, const int *bad, int bad_value,
-                      hipStream_t s);
+                      hipStream_t s, int *nonfinite = nullptr);
 // The SGD of up to kSgdBatch stores of one dtype in one launch, as
 // launch_sgd on each in sequence: store c is skipped when bad[k] != 0 for any
 // k <= first + c (its own gradient or an earlier store's is non-finite), and
@@ -70,6 +72,7 @@ struct SgdStore {
   int64_t n;
   float scale, minv;
   int code;  // the stop code when this store's gradient is the first non-finite one
+  int *nonfinite;  // E5M2: |= 1 when a new code decodes to Inf or NaN (nullable)
 };
 struct SgdBatch {
   SgdStore store[kSgdBatch];
@@ -157,49 +160,16 @@ hipError_t launch_read_probe(const void *p, int64_t bytes, uint32_t *sink, hipSt
 // (0 = auto, 1 = GEMV, 2 = MFMA GEMM, 3 = generic element-wise).
 void set_forward_path(int path);
 
-// Tuning knobs: 0 batch-1 GEMV variant (0 row-group kernel, 1 all-loads-in-
-// flight kernel, 2 column-stationary kernel), 1 column-stationary rows per
-// block (0 = default), 2 column-stationary f64 in-lane accumulation, 3 chunks
-// per lane of the all-loads kernel (0 auto, 1: 2, 2: 4, 3: 1, 4: 8).  Returns
-// the previous value (-1 for an unknown key).
-// 4 register-B forward GEMM for <= 16-bit formats (1 on), 5 its workgroups
-// per CU (0 = 2).
-// 6 hardware FP8 / FP4 converts and integer Int8 decode instead of tables (1 on),
-// 7 pair table for 4-bit formats (1 on).
-// 8 all-loads-in-flight rows per block (0 = 8 / chunks per lane; 1, 2, 4, 8, 16).
-// 9 all-loads-in-flight grid: waves per CU walking the row groups (0 = one
-// block per row group; -1 = auto: 16 for the FP8 and FP4 converter formats,
-// else 0; -k for k >= 2: k row groups per block).
-// 10 split-x bf16 MFMA GEMM for FP8 E4M3 / E5M2, Int8, FP4 and NF4 (1 on), 11 its weight
-// prefetch depth in k stages (0 auto: 1, and 2 on two-group workgroups; 1, 2, or 3 for
-// batch <= 32), 12 its block
-// width (0: 256 output columns, 1: 128).  13 dW kernel, all bit-identical to the
-// sequential FMA: 2 fp32 MFMA with operands staged in LDS (shapes of whole
-// 128-tiles; others take 1), 1 fp32 MFMA with direct loads, 0 VALU.  14 the
-// split-x GEMM's 16-row tile on the 16x16x32 MFMA for batch <= 16 (1 on).
-// 15 the split-x GEMM's two-group workgroups (8 waves sharing each unit's
-// k range, one partial tile per workgroup) for 32- and 64-row tiles of 256
-// columns when the k stages pair up (1 on).  16 for batch <= 16: forward and
-// dX without a k split across workgroups (gemm_bf3r_kernel for the split-x
-// formats' forward, gemm_regr_kernel for the others', gemm_regt_kernel for
-// every dX; epilogue in the kernel, no reduction launch): 0 off, 1 for a
-// reduction length <= 2048, 2 always.  17 in a volume training step, the
-// derivative of a piecewise activation applied in the epilogue of the layer
-// above's no-split dX instead of a launch of its own (1 on).  18 in a volume
-// training step, the SGD of consecutive stores of one dtype in one launch
-// (up to kSgdBatch per launch; 1 on, 0 one launch per store).  19 in a
-// volume training step, the dW of every layer deferred to the end of the
-// backward and launched kDwBatch layers at a time (1 on).  21 the batch <= 16
-// no-split forward and dX with x / dpre copied into LDS once per workgroup
-// (K <= 2048; 1 on).
+// Route switches (the C-ABI's welvet_hip_set_tuning documents each value):
+// 10 the split-x GEMM, 16 no-split batch <= 16 forward / dX, 17 the folded
+// activation derivative, 18 the batched SGD, 19 the batched dW, 20 the batch
+// 2-8 GEMV (k >= 2: k waves per CU), 21 the LDS-staged no-split kernels.
+// Atomic; the other key numbers are unknown (set_tuning and tuning return -1).
 enum TuneKey {
-  kTuneGemv1 = 0, kTuneRowsPerBlock = 1, kTuneAcc64 = 2, kTuneCR = 3, kTuneRegGemm = 4,
-  kTuneGemmOcc = 5, kTuneFastDecode = 6, kTunePairLut = 7, kTuneGemvRows = 8, kTuneGemvWaves = 9,
-  kTuneBf3 = 10, kTuneBf3Depth = 11, kTuneBf3Cols = 12, kTuneDwMfma = 13, kTuneBf3Small = 14,
-  kTuneBf3Groups = 15, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kTuneDwBatch = 19,
+  kTuneBf3 = 10, kTuneBf3Rows = 16, kTuneFoldDeriv = 17, kTuneSgdBatch = 18, kTuneDwBatch = 19,
   kTuneGemvBatch = 20, kTuneRegx = 21, kNumTune = 22
 };
-int set_tuning(int key, int value);
+int set_tuning(int key, int value);  // the previous value (-1 for an unknown key)
 int tuning(int key);  // the current value (-1 for an unknown key)
 
 }  // namespace wh

@@ -300,9 +300,17 @@ welvet_status store_sgd(Store *w, const float *d_dW, double lr, int *d_flag, hip
   } else if (flag) {
     return make_status(kInvalid, "weights: nonfinite gradient");
   }
-  WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, nullptr, 0, s));
-  if (w->dtype == kFP8E5M2) w->finite = false;  // an update can overflow to Inf
+  // *d_flag is 0 here (the gradient check passed); an E5M2 update sets it
+  // when a new code is Inf or NaN, which decides the store's decode route
+  const bool e5 = w->dtype == kFP8E5M2;
+  WH_HIP(launch_sgd(w->dtype, w->body, w->kbody, n, d_dW, lr, w->scale, w->minv, nullptr, nullptr, 0, s,
+                    e5 ? d_flag : nullptr));
   w->tbody_ok = false;
+  if (e5) {
+    WH_HIP(hipMemcpyAsync(&flag, d_flag, sizeof(int), hipMemcpyDeviceToHost, s));
+    WH_HIP(hipStreamSynchronize(s));
+    w->finite = flag == 0;
+  }
   return ok();
 }
 

@@ -49,7 +49,9 @@ struct welvet_hip_grid {
   float *d_x = nullptr, *d_t = nullptr, *d_gy = nullptr;
   int64_t x_elems = 0, t_elems = 0, gy_elems = 0;
   double *d_loss = nullptr;
-  int *d_flag = nullptr;  // [1] SGD stop code, [2 + i] non-finite dW of tape entry i
+  // [1] SGD stop code, [2 + i] non-finite dW of tape entry i, [2 + n + i]
+  // (n cells) an Inf / NaN code after tape entry i's E5M2 update
+  int *d_flag = nullptr;
   // tape of the last forward: cell index and the input it read
   std::vector<int> tape;
   std::vector<const float *> tape_in;
@@ -187,7 +189,7 @@ const float *tape_output(const Grid *g) { return g->cells[g->tape.back()].post; 
 welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr, double *loss,
                        float *grad_in, hipStream_t s, bool loss_only = false) {
   const int64_t ny = (int64_t)g->batch * out_width;
-  WH_HIP(hipMemsetAsync(g->d_flag, 0, (2 + g->tape.size()) * sizeof(int), s));
+  WH_HIP(hipMemsetAsync(g->d_flag, 0, (2 + 2 * g->cells.size()) * sizeof(int), s));
   WH_HIP(launch_mse(tape_output(g), d_target, ny, g->d_loss, g->d_gy, g->ws, g->ws_bytes, s));
   if (loss_only) {
     double h_loss = 0.0;
@@ -262,6 +264,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
                           (size_t)g->batch * g->cells[g->tape[0]].in * sizeof(float),
                           hipMemcpyDeviceToHost, s));
   welvet_status late = ok();  // a host-side SGD error found part-way (codes after kernel codes)
+  size_t e5_sent = 0;         // tape entries whose SGD was launched
   if (lr == 0.0) {
     late = make_status(kInvalid, "training: LR is 0");
   } else if (!std::isfinite(lr)) {
@@ -272,6 +275,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
     // this order would); a pending batch goes out before anything that
     // stops the sequence.
     const bool batched = tuning(kTuneSgdBatch) != 0;
+    int *e5_flag = g->d_flag + 2 + g->cells.size();
     SgdBatch batch{};
     int batch_dt = -1, batch_first = 0;
     auto flush = [&]() -> hipError_t {
@@ -297,22 +301,35 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
           batch_dt = c.W.dtype;
           batch_first = (int)j;
         }
-        batch.store[batch.count++] = SgdStore{c.W.body, c.W.kbody, c.dW, n, c.W.scale, c.W.minv, code};
+        batch.store[batch.count++] =
+            SgdStore{c.W.body, c.W.kbody, c.dW, n, c.W.scale, c.W.minv, code, e5_flag + j};
       } else {
         WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv,
-                          g->d_flag + 1, g->d_flag + 2 + j, code, s));
+                          g->d_flag + 1, g->d_flag + 2 + j, code, s, e5_flag + j));
       }
-      if (c.W.dtype == kFP8E5M2) c.W.finite = false;  // an update can overflow to Inf
+      e5_sent = j + 1;
       c.W.tbody_ok = false;
     }
     WH_HIP(flush());
   }
   int stop = 0;
   double h_loss = 0.0;
+  std::vector<int> e5(e5_sent, 0);
   WH_HIP(hipMemcpyAsync(&stop, g->d_flag + 1, sizeof(int), hipMemcpyDeviceToHost, s));
   WH_HIP(hipMemcpyAsync(&h_loss, g->d_loss, sizeof(double), hipMemcpyDeviceToHost, s));
+  if (e5_sent > 0)
+    WH_HIP(hipMemcpyAsync(e5.data(), g->d_flag + 2 + g->cells.size(), e5_sent * sizeof(int),
+                          hipMemcpyDeviceToHost, s));
   WH_HIP(hipStreamSynchronize(s));
   if (loss) *loss = h_loss;
+  // E5M2 stores whose SGD was launched: finite unless a new code is Inf /
+  // NaN; after a stop, a launched store may have been skipped (its codes
+  // unchanged, its flag 0), so each is marked non-finite, which is always
+  // safe (it only selects the decode that handles Inf / NaN)
+  for (size_t j = 0; j < e5_sent; ++j) {
+    Grid::Cell &c = g->cells[g->tape[j]];
+    if (c.W.dtype == kFP8E5M2) c.W.finite = stop == 0 && e5[j] == 0;
+  }
   if (lr == 0.0 || !std::isfinite(lr)) return late;  // no cell was updated
   if (stop == kUnsupported) return make_status(kUnsupported, "SGD: gradient is not a finite f32");
   if (stop == kInvalid) return make_status(kInvalid, "weights: nonfinite gradient");
@@ -428,8 +445,8 @@ welvet_status welvet_hip_grid_new(int32_t depth, int32_t rows, int32_t cols, int
     return make_status(kInternal, "hip: %s", hipGetErrorString(e));
   };
   hipError_t e = hipMalloc(&g->d_loss, sizeof(double));
-  if (e == hipSuccess) e = hipMalloc(&g->d_flag, (2 + (size_t)n) * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(g->d_flag, 0, (2 + (size_t)n) * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&g->d_flag, (2 + 2 * (size_t)n) * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(g->d_flag, 0, (2 + 2 * (size_t)n) * sizeof(int));
   if (e != hipSuccess) return fail(e);
   st = grow_ws(g, mse_workspace_bytes(0));
   if (st.code) {

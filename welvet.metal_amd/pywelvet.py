@@ -218,9 +218,8 @@ def set_forward_path(path: int) -> None:
     lib().welvet_hip_set_forward_path(path)
 
 
-TUNE = {"gemv1": 0, "rows_per_block": 1, "acc64": 2, "cr": 3, "reg_gemm": 4, "gemm_occ": 5,
-        "fast_decode": 6, "pair_lut": 7, "gemv_rows": 8, "gemv_waves": 9, "bf3": 10, "bf3_depth": 11, "bf3_cols": 12,
-        "dw_mfma": 13, "bf3_small": 14, "bf3_groups": 15, "bf3_rows": 16, "fold_deriv": 17, "sgd_batch": 18, "dw_batch": 19,
+# Route switches of welvet_hip_set_tuning (include/welvet_c.h).
+TUNE = {"bf3": 10, "bf3_rows": 16, "fold_deriv": 17, "sgd_batch": 18, "dw_batch": 19,
         "gemv_batch": 20, "regx": 21}
 
 
