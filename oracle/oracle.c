@@ -645,7 +645,7 @@ int or_set(int dt, uint8_t *raw, int64_t raw_n, float scale, int64_t i, int64_t 
   if (scale == 0) scale = 1;
   const int64_t need = or_native_bytes(dt, n);
   if (need < 0 || dt == OR_FLOAT32 || dt == OR_FLOAT64) return 1;
-  if (raw_n < need) return 1;
+  if (raw_n < need || i < 0 || i >= n) return 1;
   switch (dt) {
   case OR_FLOAT16: put_u16(raw, i * 2, or_f32_to_f16(v)); return 0;
   case OR_BFLOAT16: put_u16(raw, i * 2, or_f32_to_bf16(v)); return 0;

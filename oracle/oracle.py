@@ -13,7 +13,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(HERE, "liboracle.so")
+# WELVET_ORACLE_SO: another build of the same sources (the sanitizer build)
+ORACLE_SO = os.environ.get("WELVET_ORACLE_SO") or os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libwelvet_ref.so")
 
 # include/welvet/dtype.hpp:9-44 and src/core/dtype.cpp:5-43

@@ -191,7 +191,7 @@ welvet_status run_normalbp(bool residual, int32_t batch, int32_t seq, int32_t di
 
 bool bad_dims(int32_t batch, int32_t seq, int32_t dim, int32_t depth) {
   return batch <= 0 || seq <= 0 || dim <= 0 || depth <= 0 || (int64_t)batch * seq > INT32_MAX ||
-         (int64_t)depth * dim * dim > INT32_MAX;
+         (int64_t)dim * dim > INT32_MAX || (int64_t)depth * dim * dim > INT32_MAX;
 }
 
 }  // namespace

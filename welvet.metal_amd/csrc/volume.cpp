@@ -18,6 +18,7 @@
 #include <cfloat>
 #include <cmath>
 #include <mutex>
+#include <initializer_list>
 #include <vector>
 
 #include "runtime.hpp"
@@ -430,10 +431,13 @@ welvet_status welvet_hip_grid_new(int32_t depth, int32_t rows, int32_t cols, int
   g->cols = cols < 1 ? 1 : cols;
   g->layers = layers_per_cell < 1 ? 1 : layers_per_cell;
   g->batch = batch;
-  const int64_t n = (int64_t)g->depth * g->rows * g->cols * g->layers;
-  if (n > (1 << 20)) {
-    delete g;
-    return make_status(kInvalid, "architecture: grid too large");
+  int64_t n = 1;  // at most 2^20 cells, checked factor by factor (no overflow)
+  for (const int d : {g->depth, g->rows, g->cols, g->layers}) {
+    if (n > (int64_t(1) << 20) / d) {
+      delete g;
+      return make_status(kInvalid, "architecture: grid too large");
+    }
+    n *= d;
   }
   g->cells.resize((size_t)n);
   if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess) {

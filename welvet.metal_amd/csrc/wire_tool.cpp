@@ -20,10 +20,12 @@
 // malformed wire, 1 for an error the library reports.  Wires of the
 // reference's other layer kinds (attention, norms, convolutions, ...) are not
 // part of this build: the tool names them and exits with 2.
+#include <algorithm>
 #include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -38,10 +40,19 @@ int64_t ns_between(Clock::time_point a, Clock::time_point b) {
 }
 
 bool read_exact(void *p, size_t n) { return std::fread(p, 1, n, stdin) == n; }
+// n values, read 1 M at a time so that the vector only grows as far as the
+// wire actually holds values: a header that claims more than follows fails
+// with what was read, never with an allocation of the claimed size
 template <typename T>
 bool read_vec(std::vector<T> &v, size_t n) {
-  v.resize(n);
-  return n == 0 || read_exact(v.data(), n * sizeof(T));
+  constexpr size_t kChunk = size_t(1) << 20;
+  v.clear();
+  while (v.size() < n) {
+    const size_t at = v.size(), k = std::min(kChunk, n - at);
+    v.resize(at + k);
+    if (!read_exact(v.data() + at, k * sizeof(T))) return false;
+  }
+  return true;
 }
 template <typename T>
 bool read_one(T *p) {
@@ -278,8 +289,11 @@ int run_swiglu_normalbp(int bench_iters) {
   std::vector<float> gyt;
   if (!read_one(&use_target) || !read_vec(gyt, w.x.size()) || !read_one(&lr)) return 2;
   const size_t nw = 3 * (size_t)w.inter * w.in;
-  std::vector<float> pre((size_t)w.batch * w.seq * w.inter), post(w.x.size()), dX(w.x.size()),
-      dW(nw), W_after(nw);
+  // with in >= 1 the wire's x and gate values bound batch * seq and inter; a
+  // zero in (refused by the library) gets no outputs rather than an
+  // allocation of batch * seq * inter values no wire byte backs
+  const size_t npre = w.in > 0 ? (size_t)w.batch * w.seq * w.inter : 0;
+  std::vector<float> pre(npre), post(w.x.size()), dX(w.x.size()), dW(nw), W_after(nw);
   double loss = 0.0;
   auto step = [&]() {
     return welvet_swiglu_normalbp_f32(w.batch, w.seq, w.in, w.inter, w.dtype, w.backend,
@@ -442,7 +456,11 @@ int read_grid(GridHeader *h, const char *tag) {
 // then in, out, act, dtype, W [out][in], bias_len, bias (volume_fwd.cpp:150-170)
 int read_cells(const GridHeader &h, std::vector<CellInit> *cells, int *first_in) {
   const int D = clamp1(h.depth), R = clamp1(h.rows), Cc = clamp1(h.cols), L = clamp1(h.lpc);
-  if ((int64_t)D * R * Cc * L > (1 << 20)) return 2;
+  int64_t hops = 1;  // at most 2^20, checked factor by factor (no overflow)
+  for (const int d : {D, R, Cc, L}) {
+    if (hops > (int64_t(1) << 20) / d) return 2;
+    hops *= d;
+  }
   *first_in = -1;
   for (int z = 0; z < D; ++z)
     for (int y = 0; y < R; ++y)
