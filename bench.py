@@ -339,7 +339,7 @@ def timed_repeats(torch, stream, step, est_ms, min_ms=20.0, repeats=5, min_steps
             "steps_per_repeat": n, "repeats": repeats}
 
 
-def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, init="normal"):
+def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, init="normal", act_out=-1):
     """Forward of a Dense chain on device buffers; rotates grid copies so the
     working set exceeds the MALL.  Median of 5 repeats of >= 20 ms each."""
     import numpy as np
@@ -348,7 +348,7 @@ def time_volume_forward(torch, P, widths, dtype, batch, steps, warmup, seed, ini
     wbytes = sum(widths[i] * widths[i + 1] * bits // 8 for i in range(len(widths) - 1))
     copies = max(2, -(-MALL_BYTES // wbytes))
     shared = {}
-    grids = [_grid(P, widths, dtype, batch, rng, init, shared=shared) for _ in range(copies)]
+    grids = [_grid(P, widths, dtype, batch, rng, init, act_out=act_out, shared=shared) for _ in range(copies)]
     dev = torch.device("cuda:0")
     x = torch.randn((batch, widths[0]), device=dev)
     y = torch.empty((batch, widths[-1]), device=dev)
@@ -474,11 +474,46 @@ def time_volume_train(torch, P, dims, widths, dtype, batch, steps, seed, lr=1e-3
 FWD_WARMUP = 500
 
 
-def run_configs(torch, P, only=("c2", "c3", "c4", "c5")):
-    """BASELINE configs 2-5 (config 1 is the reference's own CPU case); `only`
-    selects configs by name prefix."""
+def c1_cpu_baseline(runs: int = 200):
+    """Config 1 as the reference runs it, on the host: the oracle's scalar port
+    of the CPU path (per-element decode switch + f64 dot, tanh) for the 1x1x1
+    volume's Dense 512 -> 512 Float32 at batch 1, one thread; median of `runs`
+    forwards after one warm-up."""
+    import numpy as np
+    from oracle import Oracle
+
+    O = Oracle()
+    rng = np.random.default_rng(0x5EED0000)
+    W = _weights(rng, 512, 512, "uniform05")
+    x = rng.standard_normal((1, 512), dtype=np.float32)
+    raw, scale = O.pack(1, W)
+    O.forward_native(1, raw, scale, x, 512, 512, 3, threads=1)
+    t = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        O.forward_native(1, raw, scale, x, 512, 512, 3, threads=1)
+        t.append(time.perf_counter() - t0)
+    t.sort()
+    return {"ms_per_step": round(t[len(t) // 2] * 1e3, 4), "cores": 1, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"median of {runs} forwards after one warm-up (per-element decode switch, "
+                      "f64 dot, tanh; 1 thread)"}
+
+
+def run_configs(torch, P, only=("c1", "c2", "c3", "c4", "c5"), cpu=True, c5_dtypes=range(34)):
+    """BASELINE configs 1-5; `only` selects configs by name prefix.  Config 1
+    is the reference's own CPU case: the GPU volume forward is timed, and with
+    `cpu` the CPU path on the host beside it."""
     out = {}
     seed = 0x5EED0000
+    if "c1" in only:
+        # 1x1x1 volume, Dense 512 -> 512 Float32, batch 1, tanh, W ~ U(-0.05, 0.05)
+        leg = time_volume_forward(torch, P, [512, 512], 1, 1, 100, FWD_WARMUP, seed, init="uniform05",
+                                  act_out=3)
+        if cpu:
+            leg["cpu_baseline"] = c1_cpu_baseline()
+            leg["gpu_speedup_vs_cpu_path"] = round(leg["cpu_baseline"]["ms_per_step"] / leg["ms_per_step"], 1)
+        out["c1_f32_512x512_b1_tanh"] = leg
     for name, dt in (("e4m3", 4), ("e5m2", 5)) if "c2" in only else ():
         for b in (1, 32):
             out[f"c2_{name}_4096x4096_b{b}"] = time_volume_forward(
@@ -506,7 +541,7 @@ def run_configs(torch, P, only=("c2", "c3", "c4", "c5")):
         out[f"c4_{name}_2048-8192-2048_b256"] = time_volume_train(
             torch, P, (1, 1, 2, 1), [2048, 8192, 2048], dt, 256, 10, seed + 3)
     c5, skipped = {}, []
-    for dt in range(34) if "c5" in only else ():
+    for dt in c5_dtypes if "c5" in only else ():
         r = time_volume_train(torch, P, (2, 2, 2, 4), [1024] * 33, dt, 16, 2, seed + 4)
         c5[P.DTYPE_NAMES[dt]] = round(r["ms_per_step"], 4)
         if r["sgd_skipped_nonfinite"]:
@@ -591,9 +626,11 @@ def main():
     ap.add_argument("--only", default="", help="comma list of cases: fp8b1,nf4b1,fp8b64,nf4b64 (the "
                     "default set), fp8b2,fp8b4,nf4b2,nf4b4 (the batch 2-4 GEMV, only when named)")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip BASELINE configs 2-5 (reported under config_results)")
-    ap.add_argument("--configs", default="c2,c3,c4,c5",
-                    help="comma list of the BASELINE configs to run: c2,c3,c4,c5")
+                    help="skip BASELINE configs 1-5 (reported under config_results)")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5",
+                    help="comma list of the BASELINE configs to run: c1,c2,c3,c4,c5")
+    ap.add_argument("--c5-dtypes", default="",
+                    help="comma list of dtype names for config 5 (default: all 34)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain copy kernel of known size (for scaling HBM counters)")
     ap.add_argument("--cpu-configs", action="store_true",
@@ -660,7 +697,9 @@ def main():
                     for k, v in results.items()},
     }
     if not a.no_configs:
-        line["config_results"] = run_configs(torch, pywelvet, tuple(a.configs.split(",")))
+        c5 = [pywelvet.DTYPE_NAMES.index(n) for n in a.c5_dtypes.split(",")] if a.c5_dtypes else range(34)
+        line["config_results"] = run_configs(torch, pywelvet, tuple(a.configs.split(",")), cpu=not a.no_cpu,
+                                             c5_dtypes=c5)
     if not a.no_cpu:
         first = 26 if prim["weight_dtype"] == "nf4" else 4
         line["cpu_baseline"] = cpu_baseline((first, 30 - first), prim["batch"])

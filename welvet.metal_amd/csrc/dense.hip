@@ -3256,7 +3256,10 @@ template <bool FWD>
 hipError_t launch_bf3r(const SkPlan &p, int bk, const GemmArgs &a, const double *bias, int bias_len,
                        int act, float *out, float *post, hipStream_t s) {
   const dim3 grid(p.gx, p.gy);
-#define WH_GR3(BK) gemm_bf3r_kernel<BK, 4, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);
+  // two rounds of weights in flight per wave (measured at batch 8-16: 1024^2
+  // FP8 5.70 against 6.24 us with four, NF4 6.49 against 7.12; eight slower
+  // still: the per-stage x split, not the load latency, bounds these)
+#define WH_GR3(BK) gemm_bf3r_kernel<BK, 2, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);
   switch (bk) {
   case BK_E4: WH_GR3(BK_E4) break;
   case BK_I8: WH_GR3(BK_I8) break;
