@@ -125,6 +125,26 @@ def test_wires_match_the_abi(oracle):
     assert rel_err(got["post"], o["post"].ravel()) <= 2e-5
 
 
+@pytest.mark.parametrize("inn", [512, 2560])
+@pytest.mark.parametrize("rows", [1, 3, 8, 40])
+@pytest.mark.parametrize("dtype", [4, 26, 1, 9])
+def test_gated_epilogue_on_every_up_route(oracle, dtype, rows, inn):
+    """op_swiglu's product runs in the Up projection's epilogue (Gate leaves
+    g in h, Up turns each element into fl32(silu(g)) * u): batch 1 (GEMV),
+    3 (batched GEMV), 8 (no-split GEMM at K = 512, the k-split GEMM and its
+    reduction at K = 2560) and 40 (32/64-row GEMM + reduction), split-x and
+    fp32-MFMA formats; h and the output against the oracle."""
+    rng = np.random.default_rng(700 + dtype + rows + inn)
+    inter = 392
+    G, U, D = _weights(rng, inter, inn, dtype)
+    x = rng.normal(0, 1, (rows, inn)).astype(np.float32)
+    print(f"swiglu gated dtype={dtype} rows={rows} in={inn}", flush=True)
+    pre, post = pywelvet.swiglu_forward(G, U, D, x, dtype=dtype)
+    o = oracle.swiglu_normalbp(dtype, G, U, D, x)
+    assert rel_err(pre, o["pre"]) <= 1e-5, rel_err(pre, o["pre"])
+    assert rel_err(post, o["post"]) <= 2e-5, rel_err(post, o["post"])
+
+
 def test_c3_shape_forward(oracle):
     """The config-3 shape 4096 -> 11008 -> 4096 as one SwiGLU (NF4 and FP4
     Gate/Up/Down) at batch 1 and 8, against the oracle."""

@@ -35,6 +35,11 @@ enum Code : int32_t { kOk = 0, kInvalid = 1, kUnsupported = 2, kGap = 3, kIntern
 // include/welvet/activate.hpp:8-17
 enum Act : int32_t { kLinear = -1, kReLU = 0, kSilu = 1, kGELU = 2, kTanh = 3, kSigmoid = 4,
                      kLeakyReLU = 5, kReLU2 = 6 };
+// Epilogue of SwiGLU's Up projection (this library's, not a reference
+// activation): post already holds the Gate projection g at each output, and
+// the epilogue writes pre = u and post = fl32(silu(g)) * u there: op_swiglu's
+// h (ops_common.metal:27-38) without a launch of its own.
+constexpr int32_t kSwiGated = 100;
 
 // Bits per element in the body (native_codec.cpp:189-560; LP64 host: Int,
 // Uint and Uintptr are 64-bit).
@@ -291,7 +296,7 @@ __device__ inline void bias_act_store(double sum, int o, const double *bias, int
   float p = (float)sum;
   if (bias != nullptr && o < bias_len) p = (float)((double)p + bias[o]);
   pre[idx] = p;
-  post[idx] = act_value(p, act);
+  post[idx] = act == kSwiGated ? act_value(post[idx], kSilu) * p : act_value(p, act);
 }
 
 }  // namespace wh

@@ -2536,7 +2536,7 @@ __global__ void __launch_bounds__(256) sk_reduce_kernel(GemmArgs a, const double
     float p = (float)sum[i];
     if constexpr (FWD) {
       if (bias != nullptr && n + i < bias_len) p = (float)((double)p + bias[n + i]);
-      qv[i] = i < nv ? act_value(p, act) : 0.0f;
+      qv[i] = i >= nv ? 0.0f : act == kSwiGated ? act_value(post[idx + i], kSilu) * p : act_value(p, act);
     } else {
       if (next_pre != nullptr && i < nv) p = p * act_prime_piecewise(next_pre[idx + i], act);
     }
@@ -2910,16 +2910,9 @@ __global__ void __launch_bounds__(256) mse_grad_kernel(const float *p, const flo
 }
 
 // --------------------------------------------------- SwiGLU element-wise
-// op_swiglu ops_common.metal:27-38, forward (c[1] == 0):
-//   h = fl32(silu(gate) * up), silu rounded to f32 first
-__global__ void __launch_bounds__(256) swiglu_fwd_kernel(const float *__restrict__ gate,
-                                                         const float *__restrict__ up, int64_t n,
-                                                         float *__restrict__ h) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    h[i] = act_value(gate[i], kSilu) * up[i];
-}
-
-// op_swiglu backward (c[1] == 1): d_up = fl32(gh * silu(gate));
+// op_swiglu ops_common.metal:27-38.  The forward's h = fl32(silu(gate)) * up
+// is the kSwiGated epilogue of the Up projection; the backward (c[1] == 1):
+// d_up = fl32(gh * silu(gate));
 // d_gate = fl32((gh * up) * silu'(gate)), the product kept wide (exact in f64)
 // and rounded once
 __global__ void __launch_bounds__(256) swiglu_bwd_kernel(const float *__restrict__ gate,
@@ -3833,12 +3826,6 @@ hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *o
 size_t mse_workspace_bytes(int64_t n) {
   (void)n;
   return 1024 * sizeof(double);
-}
-
-hipError_t launch_swiglu_fwd(const float *gate, const float *up, int64_t n, float *h, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  swiglu_fwd_kernel<<<blocks_for(n), 256, 0, s>>>(gate, up, n, h);
-  return hipGetLastError();
 }
 
 hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *gh, int64_t n,

@@ -140,9 +140,9 @@ hipError_t launch_dw_batch(const DwBatch &b, hipStream_t s);
 hipError_t launch_backward(const DevStore &w, int batch, const float *x, const float *pre,
                            const float *gy, int act, float *dpre, float *dX, float *dW, int *flag,
                            void *ws, size_t ws_bytes, hipStream_t s, const BackwardChain &chain = {});
-// SwiGLU element-wise steps (op_swiglu): h = fl32(silu(gate) * up);
-// backward d_up = fl32(gh * silu(gate)), d_gate = fl32(gh * up * silu'(gate)).
-hipError_t launch_swiglu_fwd(const float *gate, const float *up, int64_t n, float *h, hipStream_t s);
+// SwiGLU's backward element-wise step (op_swiglu): d_up = fl32(gh *
+// silu(gate)), d_gate = fl32(gh * up * silu'(gate)).  The forward product is
+// the kSwiGated epilogue of the Up projection (common.hpp).
 hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *gh, int64_t n,
                              float *d_up, float *d_gate, hipStream_t s);
 // out = fl32(a + b)

@@ -10,9 +10,9 @@
 //             dW = concat(dW_gate, dW_up, dW_down)                  (:164-252)
 //   SGD       Gate, Up, Down in that order, the first failure stops (:254-275)
 // The three stores stay packed in HBM and every step is a kernel of this
-// library (the Dense GEMV/GEMM, dX and dW kernels, op_swiglu as one
-// element-wise kernel each way); nothing round-trips through the host between
-// the layers.  The backward reuses the forward's gate, up, h and Down pre
+// library (the Dense GEMV/GEMM, dX and dW kernels; op_swiglu's forward in
+// the epilogue of the Up projection, its backward as one element-wise
+// kernel); nothing round-trips through the host between the layers.  The backward reuses the forward's gate, up, h and Down pre
 // values: the reference recomputes them with the same deterministic kernels.
 #include <hip/hip_runtime.h>
 
@@ -35,7 +35,7 @@ struct Swiglu {
   void *ws = nullptr;
   size_t ws_bytes = 0;
   std::vector<void *> bufs;
-  float *x = nullptr, *g_pre = nullptr, *g_post = nullptr, *u_pre = nullptr, *u_post = nullptr;
+  float *x = nullptr, *g_pre = nullptr, *u_pre = nullptr;
   float *h = nullptr, *d_pre = nullptr, *d_post = nullptr;
   int *flag = nullptr;
 
@@ -91,7 +91,7 @@ welvet_status make(Swiglu *L, int bs, int in, int inter, int dtype, const float 
   if (st.code == 0) st = prefixed("Down", store_from_host(&L->down, dtype, in, inter, Down, L->stream));
   if (st.code) return st;
   const int64_t nh = (int64_t)bs * inter, nx = (int64_t)bs * in;
-  for (float **p : {&L->g_pre, &L->g_post, &L->u_pre, &L->u_post, &L->h})
+  for (float **p : {&L->g_pre, &L->u_pre, &L->h})
     if ((st = L->alloc(p, nh)).code) return st;
   for (float **p : {&L->x, &L->d_pre, &L->d_post})
     if ((st = L->alloc(p, nx)).code) return st;
@@ -105,12 +105,12 @@ welvet_status make(Swiglu *L, int bs, int in, int inter, int dtype, const float 
 
 // swiglu::forward swiglu.cpp:93-141: x [bs][in] -> h [bs][inter] (the
 // layer's pre), post [bs][in], enqueued on s
+// Gate writes g to pre and to h; Up's epilogue (kSwiGated) turns each h
+// element into fl32(silu(g)) * u, op_swiglu's product, and keeps u in u_pre
+// (Linear: post = pre); then Down on h.
 welvet_status forward(Swiglu *L, const float *x, float *h, float *post, hipStream_t s) {
-  WH_HIP(launch_forward(L->gate.dev(), L->bs, x, nullptr, 0, kLinear, L->g_pre, L->g_post, L->ws,
-                        L->ws_bytes, s));
-  WH_HIP(launch_forward(L->up.dev(), L->bs, x, nullptr, 0, kLinear, L->u_pre, L->u_post, L->ws,
-                        L->ws_bytes, s));
-  WH_HIP(launch_swiglu_fwd(L->g_pre, L->u_post, (int64_t)L->bs * L->inter, h, s));
+  WH_HIP(launch_forward(L->gate.dev(), L->bs, x, nullptr, 0, kLinear, L->g_pre, h, L->ws, L->ws_bytes, s));
+  WH_HIP(launch_forward(L->up.dev(), L->bs, x, nullptr, 0, kSwiGated, L->u_pre, h, L->ws, L->ws_bytes, s));
   WH_HIP(launch_forward(L->down.dev(), L->bs, h, nullptr, 0, kLinear, L->d_pre, post, L->ws,
                         L->ws_bytes, s));
   return ok();
@@ -190,7 +190,7 @@ welvet_status welvet_swiglu_normalbp_f32(int32_t batch, int32_t seq, int32_t inp
   if ((st = store_prepare_backward(&L.down, bs, s)).code) return st;
   WH_HIP(launch_backward(L.down.dev(), bs, L.h, L.d_pre, gy, kLinear, dpre, grad_h, dw_d, L.flag,
                          L.ws, L.ws_bytes, s));
-  WH_HIP(launch_swiglu_bwd(L.g_pre, L.u_post, grad_h, nh, d_up, d_gate, s));
+  WH_HIP(launch_swiglu_bwd(L.g_pre, L.u_pre, grad_h, nh, d_up, d_gate, s));
   if ((st = store_prepare_backward(&L.gate, bs, s)).code) return st;
   WH_HIP(launch_backward(L.gate.dev(), bs, L.x, L.g_pre, d_gate, kLinear, dpre, gx_g, dw_g, L.flag,
                          L.ws, L.ws_bytes, s));
