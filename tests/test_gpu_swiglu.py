@@ -145,6 +145,24 @@ def test_gated_epilogue_on_every_up_route(oracle, dtype, rows, inn):
     assert rel_err(post, o["post"]) <= 2e-5, rel_err(post, o["post"])
 
 
+@pytest.mark.parametrize("inn,inter", [(128, 389), (1056, 389), (4096, 1024), (8192, 264)])
+@pytest.mark.parametrize("dtype", [4, 5, 26, 16, 9, 14, 15])
+def test_batch1_gate_up_one_launch(oracle, dtype, inn, inter):
+    """Batch 1: Gate and Up in one launch (x read once per block, the
+    product in the epilogue) for every format the pair kernel takes, with
+    one wave per row (the in-wave epilogue), 2-8 waves (the slice sum), a
+    ragged last wave and a partial last row group; h and the output against
+    the oracle."""
+    rng = np.random.default_rng(900 + dtype + inn + inter)
+    G, U, D = _weights(rng, inter, inn, dtype)
+    x = rng.normal(0, 1, (1, inn)).astype(np.float32)
+    print(f"swiglu pair dtype={dtype} {inn}/{inter}", flush=True)
+    pre, post = pywelvet.swiglu_forward(G, U, D, x, dtype=dtype)
+    o = oracle.swiglu_normalbp(dtype, G, U, D, x)
+    assert rel_err(pre, o["pre"]) <= 1e-5, rel_err(pre, o["pre"])
+    assert rel_err(post, o["post"]) <= 2e-5, rel_err(post, o["post"])
+
+
 def test_c3_shape_forward(oracle):
     """The config-3 shape 4096 -> 11008 -> 4096 as one SwiGLU (NF4 and FP4
     Gate/Up/Down) at batch 1 and 8, against the oracle."""

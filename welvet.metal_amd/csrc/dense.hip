@@ -765,6 +765,117 @@ __global__ void __launch_bounds__(512) gemv_loop_kernel(GemvArgs a) {
   for (int g = blockIdx.x; g < ngroups; g += gridDim.x, buf ^= 1) group(g, g == (int)blockIdx.x, buf);
 }
 
+// SwiGLU's Gate and Up projections at batch 1 in one launch (the
+// loop GEMV's structure, one chunk per lane): a row group is R rows of Gate
+// and the same R rows of Up (two stores of one format and shape; each its own
+// decode table and scale), so x is loaded once per block for both and the
+// epilogue has g and u of an output together: pre = g, pre2 = u, post = h =
+// fl32(silu(g)) * u (op_swiglu's product, ops_common.metal:27-38).  The 2R
+// sums take the fp32 butterfly as 2R rows (Gate's in rows 0..R-1, Up's in
+// R..2R-1), then the ordered f64 sum over the S slices.
+struct GemvPairArgs {
+  GemvArgs a;  // Gate: body, lut, scale, minv; x, K, N, nchunks, row_bytes; pre = g, post = h
+  const uint8_t *body2;  // Up
+  const float *lut2;
+  float scale2, minv2;
+  float *pre2;  // u
+};
+template <int F, int R>
+__global__ void __launch_bounds__(512) gemv_pair_kernel(GemvPairArgs pa) {
+  using I = FI<F>;
+  const GemvArgs &a = pa.a;
+  constexpr int E = I::kE, W = I::kW, NL = I::kTable, R2 = 2 * R;
+  constexpr int LR2 = R2 == 2 ? 1 : R2 == 4 ? 2 : R2 == 8 ? 3 : 4;
+  static_assert((1 << LR2) == R2, "2R rows: 2, 4, 8 or 16");
+  __shared__ __align__(16) float lut_s[2][NL];
+  __shared__ double part[2][8][R2];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int S = blockDim.x >> 6;
+  const int ngroups = (a.N + R - 1) / R;
+  TabCopy<F> tab, tab2;
+  if constexpr (I::kLut) {
+    tab.load(a.lut, tid);
+    tab2.load(pa.lut2, tid);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const int cbase = wave * 64 + lane;
+  float xv[E];
+  load_x<E>(a.x + (int64_t)min(cbase, a.nchunks - 1) * E, xv);
+  const bool ragged = __builtin_amdgcn_readfirstlane(wave) * 64 + 64 > a.nchunks;
+  uint32_t keep = cbase < a.nchunks ? ~0u : 0u;
+  asm volatile("" : "+v"(keep));
+  auto group = [&](int g, bool first, int buf) {
+    const int r0 = g * R;
+    uint32_t w[R2][W];
+    const int c = min(cbase, a.nchunks - 1);
+#pragma unroll
+    for (int r = 0; r < R2; ++r) {
+      const int64_t row = min(r0 + (r % R), a.N - 1);
+      const uint8_t *src = (r < R ? a.body : pa.body2) + row * a.row_bytes + (int64_t)c * (W * 4);
+      load_words_nt<W>(src, w[r]);
+    }
+    if (first) {
+      if constexpr (I::kLut) {
+        tab.store(lut_s[0], tid);
+        tab2.store(lut_s[1], tid);
+        lds_barrier();
+      }
+      if (ragged) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) xv[e] = __uint_as_float(__float_as_uint(xv[e]) & keep);
+      }
+    }
+    if constexpr (FI<F>::kMayBeNonFinite) {
+      if (ragged) {
+#pragma unroll
+        for (int r = 0; r < R2; ++r)
+#pragma unroll
+          for (int i = 0; i < W; ++i) w[r][i] &= keep;
+      }
+    }
+    float acc[R2];
+#pragma unroll
+    for (int r = 0; r < R2; ++r) {
+      float sm[4] = {0, 0, 0, 0};
+      float v[E];
+      if (r < R) decode_chunk<F>(w[r], v, lut_s[0], a.scale, a.minv);
+      else decode_chunk<F>(w[r], v, lut_s[1], pa.scale2, pa.minv2);
+#pragma unroll
+      for (int e = 0; e < E; ++e) sm[e & 3] = fmaf(v[e], xv[e], sm[e & 3]);
+      acc[r] = (sm[0] + sm[1]) + (sm[2] + sm[3]);
+    }
+    // lane l: the sum of row l >> (6 - log2 2R); Up's row r sits 32 lanes
+    // after Gate's
+    const float v = row_reduce_f32<R2>(acc, lane);
+    auto store = [&](double gs, double us, int row) {
+      const float gv = (float)gs, uv = (float)us;
+      a.pre[row] = gv;
+      pa.pre2[row] = uv;
+      a.post[row] = act_value(gv, kSilu) * uv;
+    };
+    if (S == 1) {
+      const float u = __shfl(v, (lane + 32) & 63);
+      if (lane < 32 && (lane & ((64 >> LR2) - 1)) == 0) {
+        const int row = r0 + (lane >> (6 - LR2));
+        if (row < a.N) store((double)v, (double)u, row);
+      }
+      return;
+    }
+    if ((lane & ((64 >> LR2) - 1)) == 0) part[buf][wave][lane >> (6 - LR2)] = (double)v;
+    __syncthreads();
+    if (tid < R && r0 + tid < a.N) {
+      double gs = 0, us = 0;
+      for (int q = 0; q < S; ++q) {
+        gs += part[buf][q][tid];
+        us += part[buf][q][R + tid];
+      }
+      store(gs, us, r0 + tid);
+    }
+  };
+  int buf = 0;
+  for (int g = blockIdx.x; g < ngroups; g += gridDim.x, buf ^= 1) group(g, g == (int)blockIdx.x, buf);
+}
+
 // gemv_loop_kernel for batch 2..B: the block holds the column slice of x of
 // all B batch rows in registers, so each weight chunk is loaded and decoded
 // once and feeds B products.  A row group is R rows; its R * B sums (one fp32
@@ -3573,6 +3684,39 @@ hipError_t launch_forward(const DevStore &w, int batch, const float *x, const do
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   sk_reduce_kernel<true><<<sk_reduce_grid(p), 256, 0, s>>>(a, bias, bias_len, act, pre, post, nullptr);
+  return hipGetLastError();
+}
+
+bool forward_pair_fits(const DevStore &g, const DevStore &u, int batch) {
+  if (batch != 1 || g.dtype != u.dtype || g.rows != u.rows || g.cols != u.cols) return false;
+  const int f = kernel_fmt(g.dtype);
+  if (!(f == FE4 || f == FE5 || f == FL4P || f == FF4 || f == FI8) || !chunk_aligned(g, g.cols)) return false;
+  const int nchunks = g.cols / fmt_chunk_elems(f);
+  return (nchunks + 63) / 64 <= 8;
+}
+
+hipError_t launch_forward_pair(const DevStore &g, const DevStore &u, const float *x, float *g_pre,
+                               float *u_pre, float *h, hipStream_t s) {
+  if (!forward_pair_fits(g, u, 1)) return hipErrorInvalidValue;
+  const int f = kernel_fmt(g.dtype);
+  if (kernel_body(g, f) == nullptr || kernel_body(u, f) == nullptr) return hipErrorInvalidValue;
+  GemvPairArgs pa{GemvArgs{kernel_body(g, f), g.lut, g.scale, g.minv, x, g.cols, g.rows,
+                           g.cols / fmt_chunk_elems(f), row_bytes_of(g), nullptr, 0, kLinear, g_pre, h},
+                  kernel_body(u, f), u.lut, u.scale, u.minv, u_pre};
+  // four rows of each per group, the loop GEMV's 16 waves per CU walking the
+  // groups (measured at 4096 -> 11008 against the two launches: see the
+  // SwiGLU forward)
+  constexpr int R = 4;
+  const int S = (pa.a.nchunks + 63) / 64, ngroups = (g.rows + R - 1) / R;
+  const int blocks = std::max(1, std::min(ngroups, 16 * num_cus() / S));
+  switch (f) {
+  case FE4: gemv_pair_kernel<FE4, R><<<blocks, 64 * S, 0, s>>>(pa); break;
+  case FE5: gemv_pair_kernel<FE5, R><<<blocks, 64 * S, 0, s>>>(pa); break;
+  case FL4P: gemv_pair_kernel<FL4P, R><<<blocks, 64 * S, 0, s>>>(pa); break;
+  case FF4: gemv_pair_kernel<FF4, R><<<blocks, 64 * S, 0, s>>>(pa); break;
+  case FI8: gemv_pair_kernel<FI8, R><<<blocks, 64 * S, 0, s>>>(pa); break;
+  default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

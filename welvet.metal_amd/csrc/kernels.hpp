@@ -94,6 +94,13 @@ size_t backward_workspace_bytes(const DevStore &w, int batch);
 hipError_t launch_forward(const DevStore &w, int batch, const float *x, const double *bias,
                           int bias_len, int act, float *pre, float *post, void *ws, size_t ws_bytes,
                           hipStream_t s);
+// SwiGLU's Gate and Up projections at batch 1 in one launch (two stores of
+// one format and shape): g_pre = Gate x, u_pre = Up x, h = fl32(silu(g)) * u.
+// forward_pair_fits: whether the pair kernel takes the stores (FP8, NF4 /
+// Int4 / Uint4, FP4, Int8; rows of at most 8 waves of chunks).
+bool forward_pair_fits(const DevStore &g, const DevStore &u, int batch);
+hipError_t launch_forward_pair(const DevStore &g, const DevStore &u, const float *x, float *g_pre,
+                               float *u_pre, float *h, hipStream_t s);
 // out[c][r] = in[r][c] for a rows x cols byte matrix.
 hipError_t launch_transpose_u8(const uint8_t *in, int rows, int cols, uint8_t *out, hipStream_t s);
 // True when launch_backward's dX would use the store's transposed codes

@@ -108,9 +108,15 @@ welvet_status make(Swiglu *L, int bs, int in, int inter, int dtype, const float 
 // Gate writes g to pre and to h; Up's epilogue (kSwiGated) turns each h
 // element into fl32(silu(g)) * u, op_swiglu's product, and keeps u in u_pre
 // (Linear: post = pre); then Down on h.
+// At batch 1 both projections run as one launch (x read once per block, the
+// product in its epilogue).
 welvet_status forward(Swiglu *L, const float *x, float *h, float *post, hipStream_t s) {
-  WH_HIP(launch_forward(L->gate.dev(), L->bs, x, nullptr, 0, kLinear, L->g_pre, h, L->ws, L->ws_bytes, s));
-  WH_HIP(launch_forward(L->up.dev(), L->bs, x, nullptr, 0, kSwiGated, L->u_pre, h, L->ws, L->ws_bytes, s));
+  if (forward_pair_fits(L->gate.dev(), L->up.dev(), L->bs)) {
+    WH_HIP(launch_forward_pair(L->gate.dev(), L->up.dev(), x, L->g_pre, L->u_pre, h, s));
+  } else {
+    WH_HIP(launch_forward(L->gate.dev(), L->bs, x, nullptr, 0, kLinear, L->g_pre, h, L->ws, L->ws_bytes, s));
+    WH_HIP(launch_forward(L->up.dev(), L->bs, x, nullptr, 0, kSwiGated, L->u_pre, h, L->ws, L->ws_bytes, s));
+  }
   WH_HIP(launch_forward(L->down.dev(), L->bs, h, nullptr, 0, kLinear, L->d_pre, post, L->ws,
                         L->ws_bytes, s));
   return ok();
