@@ -2452,29 +2452,31 @@ done:;
 }
 
 // The split-x GEMM for batch <= 16 with no k split across workgroups: a
-// workgroup owns 32 output columns (two waves of 16) over the whole of K,
-// and its four wave groups take every fourth 64-deep k stage (group g:
-// stages g, g + 4, ...), each staging its own stage's x parts in LDS.  At
-// the end the groups' fp32 sums meet in LDS, are added in group order in f64
-// and the epilogue (post scale, then bias and activation for the forward,
-// fl32 for dX) stores the outputs directly: no partial tiles and no
-// reduction launch.  Operand layout, x split and weight decode are
-// gemm_bf3s_kernel's (16x16x32 MFMA; a lane holds 16 consecutive weights of
-// one column per stage).  Rounds past a group's last stage re-read a valid
-// stage against x masked to zero.
-template <int BK, int D, bool FWD>
-__global__ void __launch_bounds__(512) gemm_bf3r_kernel(GemmArgs a, const double *bias, int bias_len,
-                                                        int act, float *out, float *post) {
+// workgroup owns 16 * CW output columns (CW waves of 16) over the whole of K,
+// and its KG wave groups take every KG-th 64-deep k stage (group g: stages
+// g, g + KG, ...), each staging its own stage's x parts in LDS.  At the end
+// the groups' fp32 sums meet in LDS, are added in group order in f64 and the
+// epilogue (post scale, then bias and activation for the forward, fl32 for
+// dX) stores the outputs directly: no partial tiles and no reduction
+// launch.  Operand layout, x split and weight decode are gemm_bf3s_kernel's
+// (16x16x32 MFMA; a lane holds 16 consecutive weights of one column per
+// stage).  Rounds past a group's last stage re-read a valid stage against x
+// masked to zero.  NB = 1 (one x buffer per group) only when every group
+// has a single round (nst <= KG).
+template <int BK, int D, bool FWD, int KG, int CW, int NB>
+__global__ void __launch_bounds__(64 * KG * CW) gemm_bf3r_kernel(GemmArgs a, const double *bias,
+                                                                 int bias_len, int act, float *out,
+                                                                 float *post) {
   using K3 = B3<BK>;
-  constexpr int KG = 4, CW = 2, BM = 16, NW = K3::kWords / 2, NP = K3::kParts;
-  constexpr int XE = BM * kBK / 128;  // 8 x values per thread per stage (128 threads per group)
-  constexpr int XT = kBK / XE;        // 8 threads per x row
-  static_assert(XE == 8 && (NW == 2 || NW == 4), "16-row split-x layout");
-  __shared__ uint16_t Xs[2][KG][3][BM][kBf3Row];
+  constexpr int BM = 16, NW = K3::kWords / 2, NP = K3::kParts;
+  constexpr int XE = BM * kBK / (64 * CW);  // x values per thread per stage: 8 (CW = 2) or 16
+  constexpr int XT = kBK / XE;              // threads per x row
+  static_assert((XE == 8 || XE == 16) && (NW == 2 || NW == 4), "16-row split-x layout");
+  __shared__ uint16_t Xs[NB][KG][3][BM][kBf3Row];
   __shared__ float ex[KG - 1][CW][4][64];
   __shared__ uint2 t3[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int grp = wv / CW, cw = wv % CW, gt = tid & 127;
+  const int grp = wv / CW, cw = wv % CW, gt = tid & (64 * CW - 1);
   const int j = lane & 15, g = lane >> 4;
   if constexpr (BK == BK_NF4) {
     if (tid < 16) {  // NF4 table values split exactly into three bf16 parts
@@ -2510,9 +2512,11 @@ __global__ void __launch_bounds__(512) gemm_bf3r_kernel(GemmArgs a, const double
     const bool in = m0 + xm < a.M && k0 + xk < a.K;
     in_mask = in ? ~0u : 0u;
     const float *src = a.A + (int64_t)(in ? m0 + xm : 0) * a.K + (in ? k0 + xk : 0);
-    const float4 v0 = *(const float4 *)src, v1 = *(const float4 *)(src + 4);
-    xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
-    xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+#pragma unroll
+    for (int q4 = 0; q4 < XE / 4; ++q4) {
+      const float4 v = *(const float4 *)(src + 4 * q4);
+      xv[4 * q4] = v.x; xv[4 * q4 + 1] = v.y; xv[4 * q4 + 2] = v.z; xv[4 * q4 + 3] = v.w;
+    }
   };
   auto store_x = [&](int buf, const float (&xv)[XE], uint32_t in_mask) {
     uint32_t wp[3][XE / 2];
@@ -2534,7 +2538,10 @@ __global__ void __launch_bounds__(512) gemm_bf3r_kernel(GemmArgs a, const double
     }
 #pragma unroll
     for (int p = 0; p < 3; ++p)
-      *(uint4 *)&Xs[buf][grp][p][xm][xk] = make_uint4(wp[p][0], wp[p][1], wp[p][2], wp[p][3]);
+#pragma unroll
+      for (int h = 0; h < XE / 8; ++h)
+        *(uint4 *)&Xs[buf][grp][p][xm][xk + 8 * h] =
+            make_uint4(wp[p][4 * h], wp[p][4 * h + 1], wp[p][4 * h + 2], wp[p][4 * h + 3]);
   };
   floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto mfma_step = [&](int buf, int q, const bf16x8 (&bv)[NP]) {
@@ -2567,9 +2574,11 @@ __global__ void __launch_bounds__(512) gemm_bf3r_kernel(GemmArgs a, const double
       load_w(min(r + D, last), wr[d]);
 #pragma unroll
       for (int q = 0; q < 2; ++q) mfma_step(buf, q, bv[q]);
-      store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
-      lds_barrier();
-      buf ^= 1;
+      if constexpr (NB == 2) {  // NB = 1: this was the group's only round
+        store_x(buf ^ 1, xf[(d + 1) % D], xin[(d + 1) % D]);
+        lds_barrier();
+        buf ^= 1;
+      }
     }
   }
 done:
@@ -3359,11 +3368,25 @@ size_t forward_workspace_bytes(const DevStore &w, int batch) {
 template <bool FWD>
 hipError_t launch_bf3r(const SkPlan &p, int bk, const GemmArgs &a, const double *bias, int bias_len,
                        int act, float *out, float *post, hipStream_t s) {
-  const dim3 grid(p.gx, p.gy);
-  // two rounds of weights in flight per wave (measured at batch 8-16: 1024^2
-  // FP8 5.70 against 6.24 us with four, NF4 6.49 against 7.12; eight slower
-  // still: the per-stage x split, not the load latency, bounds these)
-#define WH_GR3(BK) gemm_bf3r_kernel<BK, 2, FWD><<<grid, 512, 0, s>>>(a, bias, bias_len, act, out, post);
+  // Shapes (measured at batch 8-16): K of at most 16 stages on 16 wave groups
+  // of one stage each, 16 columns per workgroup (1024^2 b16: FP8 5.78 -> 5.17
+  // us, NF4 6.70 -> 5.58, FP4 5.82 -> 4.96; five 1024^2 layers FP8 24.7 ->
+  // 21.6); longer K on 8 groups of 16 columns, two rounds of weights in
+  // flight (2048 -> 1024 b16 FP8 8.94 -> 7.95, NF4 9.84 -> 8.32; 4096 ->
+  // 11008 -> 4096 b8 NF4 68.1 -> 65.7 against 4 groups of 32 columns).  A
+  // deeper ring is slower (1024^2 FP8 5.70 us with two rounds, 6.24 with four,
+  // 7.5 with eight): the per-stage x split, not the load latency, bounds
+  // these.  Rows of x split into 16-value pieces need K % 16 == 0; other K
+  // keep 4 groups of 32 columns.
+  const dim3 grid32(p.gx, p.gy), grid16((a.N + 15) / 16, p.gy);
+  const int shape = a.K % 16 != 0 ? 0 : a.nst <= 16 ? 1 : 2;
+#define WH_GR3(BK)                                                                                        \
+  if (shape == 1)                                                                                         \
+    gemm_bf3r_kernel<BK, 1, FWD, 16, 1, 1><<<grid16, 1024, 0, s>>>(a, bias, bias_len, act, out, post);    \
+  else if (shape == 2)                                                                                    \
+    gemm_bf3r_kernel<BK, 2, FWD, 8, 1, 2><<<grid16, 512, 0, s>>>(a, bias, bias_len, act, out, post);      \
+  else                                                                                                    \
+    gemm_bf3r_kernel<BK, 2, FWD, 4, 2, 2><<<grid32, 512, 0, s>>>(a, bias, bias_len, act, out, post);
   switch (bk) {
   case BK_E4: WH_GR3(BK_E4) break;
   case BK_I8: WH_GR3(BK_I8) break;
