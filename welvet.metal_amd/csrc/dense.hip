@@ -3012,8 +3012,9 @@ __global__ void __launch_bounds__(256) mse_partial_kernel(const float *p, const 
 }
 
 __global__ void __launch_bounds__(256) mse_final_kernel(const double *part, int nparts, int64_t n,
-                                                        double *loss) {
+                                                        double *loss, int *clear, int64_t nclear) {
   __shared__ double red[4];
+  for (int64_t i = threadIdx.x; i < nclear; i += 256) clear[i] = 0;
   double s = 0;
   for (int i = threadIdx.x; i < nparts; i += 256) s += part[i];
   s = wave_sum(s);
@@ -4041,13 +4042,14 @@ hipError_t launch_read_probe(const void *p, int64_t bytes, uint32_t *sink, hipSt
 }
 
 hipError_t launch_mse(const float *pred, const float *target, int64_t n, double *loss, float *grad,
-                      void *ws, size_t ws_bytes, hipStream_t s) {
+                      void *ws, size_t ws_bytes, hipStream_t s, int *clear, int64_t nclear) {
   if (ws_bytes < mse_workspace_bytes(n)) return hipErrorInvalidValue;
+  if (nclear > 0 && (clear == nullptr || loss == nullptr)) return hipErrorInvalidValue;
   if (loss != nullptr) {
     int parts = blocks_for(n);
     if (parts > 1024) parts = 1024;
     mse_partial_kernel<<<parts, 256, 0, s>>>(pred, target, n, (double *)ws);
-    mse_final_kernel<<<1, 256, 0, s>>>((const double *)ws, parts, n, loss);
+    mse_final_kernel<<<1, 256, 0, s>>>((const double *)ws, parts, n, loss, clear, nclear > 0 ? nclear : 0);
   }
   if (grad != nullptr) mse_grad_kernel<<<blocks_for(n), 256, 0, s>>>(pred, target, n, grad);
   return hipGetLastError();

@@ -154,9 +154,11 @@ hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *gh
                              float *d_up, float *d_gate, hipStream_t s);
 // out = fl32(a + b)
 hipError_t launch_add(const float *a, const float *b, int64_t n, float *out, hipStream_t s);
-// loss = sum (p - t)^2 / n (f64);  grad = fl32(2 (p - t) / n).
+// loss = sum (p - t)^2 / n (f64);  grad = fl32(2 (p - t) / n).  With
+// nclear > 0 the loss launch also zeroes the nclear ints at clear (a step's
+// flags, cleared before the launches that follow on the stream; needs loss).
 hipError_t launch_mse(const float *pred, const float *target, int64_t n, double *loss, float *grad,
-                      void *ws, size_t ws_bytes, hipStream_t s);
+                      void *ws, size_t ws_bytes, hipStream_t s, int *clear = nullptr, int64_t nclear = 0);
 size_t mse_workspace_bytes(int64_t n);
 
 // Reads `bytes` (a multiple of 16) at p once, 16 bytes per load; sink: 1024

@@ -49,9 +49,15 @@ struct welvet_hip_grid {
   int64_t dpre_elems = 0;
   float *d_x = nullptr, *d_t = nullptr, *d_gy = nullptr;
   int64_t x_elems = 0, t_elems = 0, gy_elems = 0;
+  // A training step's status block, one device allocation: the loss (f64)
+  // at byte 0, then the flags from byte 8 — [1] SGD stop code, [2 + i] an
+  // Inf / NaN code after tape entry i's E5M2 update, [2 + n + i] (n cells)
+  // non-finite dW of tape entry i.  The step clears the flags in its loss
+  // kernel and ends with one copy of the block's head into the pinned
+  // mirror h_status.
+  void *d_status = nullptr;
+  void *h_status = nullptr;
   double *d_loss = nullptr;
-  // [1] SGD stop code, [2 + i] non-finite dW of tape entry i, [2 + n + i]
-  // (n cells) an Inf / NaN code after tape entry i's E5M2 update
   int *d_flag = nullptr;
   // tape of the last forward: cell index and the input it read
   std::vector<int> tape;
@@ -89,9 +95,9 @@ void grid_free(Grid *g) {
   if (g->stream) (void)hipStreamSynchronize(g->stream);
   for (auto &c : g->cells) free_cell(&c);
   for (void *p : {(void *)g->ws, (void *)g->gx[0], (void *)g->gx[1], (void *)g->dpre,
-                  (void *)g->d_x, (void *)g->d_t, (void *)g->d_gy, (void *)g->d_loss,
-                  (void *)g->d_flag})
+                  (void *)g->d_x, (void *)g->d_t, (void *)g->d_gy, g->d_status})
     if (p) (void)hipFree(p);
+  if (g->h_status) (void)hipHostFree(g->h_status);
   if (g->stream) (void)hipStreamDestroy(g->stream);
   delete g;
 }
@@ -190,23 +196,32 @@ const float *tape_output(const Grid *g) { return g->cells[g->tape.back()].post; 
 welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr, double *loss,
                        float *grad_in, hipStream_t s, bool loss_only = false) {
   const int64_t ny = (int64_t)g->batch * out_width;
-  WH_HIP(hipMemsetAsync(g->d_flag, 0, (2 + 2 * g->cells.size()) * sizeof(int), s));
-  WH_HIP(launch_mse(tape_output(g), d_target, ny, g->d_loss, g->d_gy, g->ws, g->ws_bytes, s));
+  const size_t ncells = g->cells.size();
+  // the loss, and the flags the step clears in the loss kernel (before any
+  // backward launch)
+  WH_HIP(launch_mse(tape_output(g), d_target, ny, g->d_loss, g->d_gy, g->ws, g->ws_bytes, s, g->d_flag,
+                    (int64_t)(2 + 2 * ncells)));
+  // one copy of the status block's head (the loss and `flags` flags) to the
+  // pinned mirror, then the step's only synchronisation
+  auto read_status = [&](size_t flags) -> hipError_t {
+    hipError_t e = hipMemcpyAsync(g->h_status, g->d_status, sizeof(double) + flags * sizeof(int),
+                                  hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e;
+  };
+  const double *h_loss = (const double *)g->h_status;
+  const int *h_flag = (const int *)((const char *)g->h_status + sizeof(double));
   if (loss_only) {
-    double h_loss = 0.0;
-    WH_HIP(hipMemcpyAsync(&h_loss, g->d_loss, sizeof(double), hipMemcpyDeviceToHost, s));
-    WH_HIP(hipStreamSynchronize(s));
-    if (loss) *loss = h_loss;
+    WH_HIP(read_status(0));
+    if (loss) *loss = *h_loss;
     return ok();
   }
   // the gradient a step passes back must fit the step before it in the tape
   // (a remote hop can break the chain: dense::backward_f32 dense.cpp:171-178)
   for (size_t i = g->tape.size() - 1; i > 0; --i) {
     if (g->cells[g->tape[i]].in != g->cells[g->tape[i - 1]].out) {
-      double h_loss = 0.0;
-      WH_HIP(hipMemcpyAsync(&h_loss, g->d_loss, sizeof(double), hipMemcpyDeviceToHost, s));
-      WH_HIP(hipStreamSynchronize(s));
-      if (loss) *loss = h_loss;
+      WH_HIP(read_status(0));
+      if (loss) *loss = *h_loss;
       return make_status(kInvalid, "dense: bwd shape mismatch");
     }
   }
@@ -222,6 +237,7 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
   // layers too small to fill the GPU wait until the walk is done and run a
   // batch at a time: the walk is then only the chain of dX launches.
   const bool batch_dw = tuning(kTuneDwBatch) != 0;
+  int *const dw_flag = g->d_flag + 2 + ncells, *const e5_flag = g->d_flag + 2;
   DwBatch dwb{};
   dwb.batch = g->batch;
   const float *gy = g->d_gy;
@@ -248,9 +264,9 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
     chain.defer_dw = batch_dw && dw_defer_pays(c.W.dev());
     chain.dpre_out = &dpre;
     WH_HIP(launch_backward(c.W.dev(), g->batch, g->tape_in[i], c.pre, gy, c.act, batch_dw ? c.grad : g->dpre,
-                           gx, c.dW, g->d_flag + 2 + i, g->ws, g->ws_bytes, s, chain));
+                           gx, c.dW, dw_flag + i, g->ws, g->ws_bytes, s, chain));
     if (chain.defer_dw) {
-      dwb.job[dwb.count++] = DwJob{dpre, g->tape_in[i], c.W.rows, c.W.cols, c.dW, g->d_flag + 2 + i};
+      dwb.job[dwb.count++] = DwJob{dpre, g->tape_in[i], c.W.rows, c.W.cols, c.dW, dw_flag + i};
       if (dwb.count == kDwBatch) {
         WH_HIP(launch_dw_batch(dwb, s));
         dwb.count = 0;
@@ -276,12 +292,11 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
     // this order would); a pending batch goes out before anything that
     // stops the sequence.
     const bool batched = tuning(kTuneSgdBatch) != 0;
-    int *e5_flag = g->d_flag + 2 + g->cells.size();
     SgdBatch batch{};
     int batch_dt = -1, batch_first = 0;
     auto flush = [&]() -> hipError_t {
       if (batch.count == 0) return hipSuccess;
-      const hipError_t e = launch_sgd_batch(batch_dt, batch, lr, g->d_flag + 1, g->d_flag + 2, batch_first, s);
+      const hipError_t e = launch_sgd_batch(batch_dt, batch, lr, g->d_flag + 1, dw_flag, batch_first, s);
       batch.count = 0;
       return e;
     };
@@ -306,23 +321,17 @@ welvet_status run_step(Grid *g, const float *d_target, int out_width, double lr,
             SgdStore{c.W.body, c.W.kbody, c.dW, n, c.W.scale, c.W.minv, code, e5_flag + j};
       } else {
         WH_HIP(launch_sgd(c.W.dtype, c.W.body, c.W.kbody, n, c.dW, lr, c.W.scale, c.W.minv,
-                          g->d_flag + 1, g->d_flag + 2 + j, code, s, e5_flag + j));
+                          g->d_flag + 1, dw_flag + j, code, s, e5_flag + j));
       }
       e5_sent = j + 1;
       c.W.tbody_ok = false;
     }
     WH_HIP(flush());
   }
-  int stop = 0;
-  double h_loss = 0.0;
-  std::vector<int> e5(e5_sent, 0);
-  WH_HIP(hipMemcpyAsync(&stop, g->d_flag + 1, sizeof(int), hipMemcpyDeviceToHost, s));
-  WH_HIP(hipMemcpyAsync(&h_loss, g->d_loss, sizeof(double), hipMemcpyDeviceToHost, s));
-  if (e5_sent > 0)
-    WH_HIP(hipMemcpyAsync(e5.data(), g->d_flag + 2 + g->cells.size(), e5_sent * sizeof(int),
-                          hipMemcpyDeviceToHost, s));
-  WH_HIP(hipStreamSynchronize(s));
-  if (loss) *loss = h_loss;
+  WH_HIP(read_status(2 + e5_sent));
+  const int stop = h_flag[1];
+  const int *e5 = h_flag + 2;
+  if (loss) *loss = *h_loss;
   // E5M2 stores whose SGD was launched: finite unless a new code is Inf /
   // NaN; after a stop, a launched store may have been skipped (its codes
   // unchanged, its flag 0), so each is marked non-finite, which is always
@@ -448,10 +457,13 @@ welvet_status welvet_hip_grid_new(int32_t depth, int32_t rows, int32_t cols, int
     grid_free(g);
     return make_status(kInternal, "hip: %s", hipGetErrorString(e));
   };
-  hipError_t e = hipMalloc(&g->d_loss, sizeof(double));
-  if (e == hipSuccess) e = hipMalloc(&g->d_flag, (2 + 2 * (size_t)n) * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(g->d_flag, 0, (2 + 2 * (size_t)n) * sizeof(int));
+  const size_t status_bytes = sizeof(double) + (2 + 2 * (size_t)n) * sizeof(int);
+  hipError_t e = hipMalloc(&g->d_status, status_bytes);
+  if (e == hipSuccess) e = hipMemset(g->d_status, 0, status_bytes);
+  if (e == hipSuccess) e = hipHostMalloc(&g->h_status, status_bytes, hipHostMallocDefault);
   if (e != hipSuccess) return fail(e);
+  g->d_loss = (double *)g->d_status;
+  g->d_flag = (int *)((char *)g->d_status + sizeof(double));
   st = grow_ws(g, mse_workspace_bytes(0));
   if (st.code) {
     grid_free(g);
