@@ -201,3 +201,34 @@ def test_grid_session_trains_at_two_batches(oracle):
             for got, co in zip(wire.read_nws1(m.export()[1])[0], order):
                 c = V.cells[co]
                 _check_store(got, c["raw"], c["scale"], c["dtype"], f"batch {batch} {co}")
+
+
+@pytest.mark.parametrize("dtype", [1, 2, 4, 5, 7, 9, 14, 26, 33],
+                         ids=["f32", "f16", "e4m3", "e5m2", "int32", "int8", "int4", "nf4", "uint3"])
+def test_stack_apply_sgd_unaligned_slices(oracle, dtype):
+    """apply_sgd on a Stack whose children's dW slices of the one gradient
+    tensor start off 16-byte boundaries (15 and 50 floats in): each child's
+    SGD takes the one-element-per-thread kernel and its stored bytes equal the
+    oracle's re-encode exactly."""
+    from parity import assert_bit_equal
+
+    rng = np.random.default_rng(3100 + dtype)
+    layers = [(rng.normal(0, 0.3, (5, 3)).astype(np.float32), -1, dtype, None),
+              (rng.normal(0, 0.3, (7, 5)).astype(np.float32), -1, dtype, None),
+              (rng.normal(0, 0.3, (6, 7)).astype(np.float32), -1, dtype, None)]
+    S = _oracle_stack(oracle, layers)
+    dwt = rng.normal(0, 0.5, 15 + 35 + 42).astype(np.float32)
+    with pywelvet.Model(model_desc.stack(oracle, layers)) as m:
+        assert m.apply_sgd(0.25, wire.tensor(dwt.reshape(1, -1))).code == 0
+        stores, _ = wire.read_nws1(m.export()[1])
+    assert S.apply_sgd(dwt, 0.25) == 0
+    moved = 0
+    for i, (got, c) in enumerate(zip(stores, S.children)):
+        if dtype == 1:
+            assert_bit_equal(got["f32"], c["raw"].view(np.float32), f"child {i}")
+            moved += int(np.count_nonzero(got["f32"] != layers[i][0].ravel()))
+            continue
+        assert got["scale"] == np.float32(c["scale"]), i
+        assert_bit_equal(got["raw"], c["raw"], f"child {i}")
+        moved += int(np.count_nonzero(got["raw"] != oracle.pack(dtype, layers[i][0])[0]))
+    assert moved > 0

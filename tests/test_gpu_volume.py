@@ -357,6 +357,44 @@ def test_train_batched_sgd_and_dw_match_per_cell(oracle, dtypes, widths, xs, lr)
             assert_bit_equal(runs[knobs][1][co], runs[(1, 1)][1][co], f"store {co} knobs {knobs}")
 
 
+GROUPED_SGD = [2, 3, 7, 8, 11, 12, 14, 15, 16, 17, 18, 19, 20, 26, 27, 28, 29, 30, 31, 32, 33]
+
+
+@pytest.mark.parametrize("dtype", GROUPED_SGD, ids=[pywelvet.DTYPE_NAMES[d] for d in GROUPED_SGD])
+def test_batched_grouped_sgd_matches_per_cell(oracle, dtype):
+    """The formats whose SGD runs several whole code words per thread: one
+    batched SGD launch over three cells of ragged sizes (tails of 1-31
+    elements past the last whole group, several blocks for the largest)
+    stores the same bytes as a launch per cell, whose kernel the codec
+    tests pin to the oracle for every dtype."""
+    from parity import assert_bit_equal
+
+    rng = np.random.default_rng(2800 + dtype)
+    widths = [257, 97, 131, 40]
+    spec = {(0, 0, l, 0): (rng.normal(0, 0.15, (widths[l + 1], widths[l])).astype(np.float32),
+                           0 if l < 2 else -1, dtype, None) for l in range(3)}
+    x = (rng.normal(0, 1, (4, widths[0])) * 0.2).astype(np.float32)
+    t = rng.normal(0, 1, (4, widths[-1])).astype(np.float32)
+    runs = {}
+    for knob in (1, 0):
+        old = pywelvet.set_tuning("sgd_batch", knob)
+        try:
+            G, _ = build(oracle, (1, 1, 3, 1), 4, spec)
+            with G:
+                before = [G.native(co)[0].copy() for co in spec]
+                # a rate large enough that the coarse formats' codes move
+                lr = 5e-2 if pywelvet.dtype_bits(dtype) >= 16 else 50.0
+                st, loss, _ = G.train_step(x, t, lr, status=True)
+                runs[knob] = (st.code, loss, before, [G.native(co)[0].copy() for co in spec])
+        finally:
+            pywelvet.set_tuning("sgd_batch", old)
+    assert runs[1][:2] == runs[0][:2]
+    for i, co in enumerate(spec):
+        assert_bit_equal(runs[1][3][i], runs[0][3][i], f"{pywelvet.DTYPE_NAMES[dtype]} store {co}")
+    if runs[1][0] == 0:
+        assert any((runs[1][3][i] != runs[1][2][i]).any() for i in range(3))
+
+
 @pytest.mark.parametrize("sgd_batch", [1, 0])
 def test_train_e5m2_overflow_then_forward(oracle, sgd_batch):
     """E5M2 cells after training steps, batch 8 (where a finite E5M2 store

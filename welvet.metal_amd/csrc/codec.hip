@@ -257,56 +257,161 @@ __device__ inline bool sgd_stopped(int *stop, const int *bad, int bad_value) {
 // The SGD element loops below take their block index and block count as
 // arguments: one launch per store (the block grid) or one launch for several
 // stores (sgd_batch_kernel: blockIdx.y picks the store).
+// The SGD of unit u (unit_elems elements, so no two threads touch a byte).
 template <int DT>
-__device__ inline void sgd_units(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
-                                 const float *__restrict__ g, double lr, float scale, float minv,
-                                 int64_t blk, int64_t nblk) {
+__device__ inline void sgd_unit(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
+                                const float *__restrict__ g, double lr, float scale, float minv, int64_t u) {
   constexpr int bits = dtype_bits(DT);
   constexpr int U = unit_elems<DT>();
-  const int64_t units = (n + U - 1) / U;
-  for (int64_t u = blk * kThreads + threadIdx.x; u < units; u += nblk * kThreads) {
-    if constexpr (bits >= 8) {
-      const uint64_t c = fix_code<DT>(sgd_value<DT>(load_code<DT>(body, u), u, g[u], lr, scale, minv),
-                                      scale, minv);
-      constexpr int fb = fix_bytes<DT>();
-      if constexpr (has_kcopy<DT>()) kbody[u] = kcode<DT>((uint32_t)c);
-      if constexpr (fb == 1) body[u] = (uint8_t)c;
-      else if constexpr (fb == 2) ((uint16_t *)body)[u] = (uint16_t)c;
-      else if constexpr (fb == 4) ((uint32_t *)(body + u * (bits / 8)))[0] = (uint32_t)c;
-      else {
-        uint32_t *p = (uint32_t *)(body + u * (bits / 8));
-        p[0] = (uint32_t)c;
-        p[1] = (uint32_t)(c >> 32);
-      }
-    } else {
-      constexpr int ubytes = U * bits / 8;
-      uint64_t acc = 0;
-#pragma unroll
-      for (int b = 0; b < ubytes; ++b) acc |= (uint64_t)body[u * ubytes + b] << (8 * b);
-      constexpr uint64_t mask = (1ull << bits) - 1;
-#pragma unroll
-      for (int j = 0; j < U; ++j) {
-        const int64_t i = u * U + j;
-        if (i < n) {
-          const uint64_t c = (acc >> (j * bits)) & mask;
-          const uint64_t nc = fix_code<DT>(sgd_value<DT>(c, i, g[i], lr, scale, minv), scale, minv);
-          acc = (acc & ~(mask << (j * bits))) | ((nc & mask) << (j * bits));
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < ubytes; ++b) body[u * ubytes + b] = (uint8_t)(acc >> (8 * b));
+  if constexpr (bits >= 8) {
+    const uint64_t c = fix_code<DT>(sgd_value<DT>(load_code<DT>(body, u), u, g[u], lr, scale, minv),
+                                    scale, minv);
+    constexpr int fb = fix_bytes<DT>();
+    if constexpr (has_kcopy<DT>()) kbody[u] = kcode<DT>((uint32_t)c);
+    if constexpr (fb == 1) body[u] = (uint8_t)c;
+    else if constexpr (fb == 2) ((uint16_t *)body)[u] = (uint16_t)c;
+    else if constexpr (fb == 4) ((uint32_t *)(body + u * (bits / 8)))[0] = (uint32_t)c;
+    else {
+      uint32_t *p = (uint32_t *)(body + u * (bits / 8));
+      p[0] = (uint32_t)c;
+      p[1] = (uint32_t)(c >> 32);
     }
+  } else {
+    constexpr int ubytes = U * bits / 8;
+    uint64_t acc = 0;
+#pragma unroll
+    for (int b = 0; b < ubytes; ++b) acc |= (uint64_t)body[u * ubytes + b] << (8 * b);
+    constexpr uint64_t mask = (1ull << bits) - 1;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t i = u * U + j;
+      if (i < n) {
+        const uint64_t c = (acc >> (j * bits)) & mask;
+        const uint64_t nc = fix_code<DT>(sgd_value<DT>(c, i, g[i], lr, scale, minv), scale, minv);
+        acc = (acc & ~(mask << (j * bits))) | ((nc & mask) << (j * bits));
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < ubytes; ++b) body[u * ubytes + b] = (uint8_t)(acc >> (8 * b));
   }
 }
 
 template <int DT>
+__device__ inline void sgd_units(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
+                                 const float *__restrict__ g, double lr, float scale, float minv,
+                                 int64_t blk, int64_t nblk) {
+  constexpr int U = unit_elems<DT>();
+  const int64_t units = (n + U - 1) / U;
+  for (int64_t u = blk * kThreads + threadIdx.x; u < units; u += nblk * kThreads)
+    sgd_unit<DT>(body, kbody, n, g, lr, scale, minv, u);
+}
+
+// Elements per thread of sgdw_units: a whole number of 32-bit code words —
+// 16 (`bits` / 2 words) for the 2-, 4- and 6-bit formats, 32 (`bits` words)
+// for the 1-, 3- and 5-bit ones, 8 for the 16-bit ones, 4 for Int32 /
+// Uint32; 0 where it does not apply.
+template <int DT>
+__host__ __device__ constexpr int sgdw_group() {
+  constexpr int b = dtype_bits(DT);
+  if (DT == kFloat32 || has_kcopy<DT>()) return 0;
+  if (b < 8) return b % 2 == 0 ? 16 : 32;
+  if (b == 16 && fix_bytes<DT>() == 2) return 8;
+  if (b == 32 && fix_bytes<DT>() == 4) return 4;
+  return 0;
+}
+
+// sgd_units over groups of sgdw_group<DT>() elements per thread: the codes
+// of a group are whole words (loaded and stored as such, every bit of them
+// rewritten), the gradient is read as float4; the elements past the last
+// whole group go unit by unit through block 0.  The per-element arithmetic
+// is sgd_units'.  FP4 / NF4 decode through a copy of their 16 values in LDS
+// (a lookup in the constant table takes 16 registers per element in
+// flight); every thread of the block must call this.
+template <int DT>
+__device__ __forceinline__ void sgdw_units(uint8_t *__restrict__ body, int64_t n, const float *__restrict__ g,
+                                  double lr, float scale, float minv, int64_t blk, int64_t nblk) {
+  constexpr int bits = dtype_bits(DT), G = sgdw_group<DT>(), NW = G * bits / 32;
+  static_assert(G > 0 && G % 4 == 0 && G * bits % 32 == 0 && G % unit_elems<DT>() == 0,
+                "whole words and units per group");
+  constexpr uint32_t mask = bits >= 32 ? ~0u : (1u << bits) - 1;
+  constexpr bool kTab = DT == kFP4 || DT == kNF4;
+  __shared__ float tab[kTab ? 16 : 1];
+  if constexpr (kTab) {
+    if (threadIdx.x < 16) tab[threadIdx.x] = dec_code<DT>(threadIdx.x, scale, minv);
+    __syncthreads();
+  }
+  auto value = [&](uint32_t c, int64_t i, float gj) {
+    if constexpr (kTab) {
+      float old = tab[c];
+      if (i == 0) old = dec_code<DT>(fix_code<DT>(old, scale, minv), scale, minv);
+      return (float)((double)old - lr * (double)gj);
+    } else {
+      return sgd_value<DT>(c, i, gj, lr, scale, minv);
+    }
+  };
+  const int64_t groups = n / G;
+  for (int64_t q = blk * kThreads + threadIdx.x; q < groups; q += nblk * kThreads) {
+    uint32_t *words = (uint32_t *)(body + q * (NW * 4));
+    uint32_t cw[NW + 1];
+    if constexpr (NW == 4) {
+      const uint4 v = *(const uint4 *)words;
+      cw[0] = v.x; cw[1] = v.y; cw[2] = v.z; cw[3] = v.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < NW; ++k) cw[k] = words[k];
+    }
+    cw[NW] = 0;
+    float gv[G];
+#pragma unroll
+    for (int v = 0; v < G / 4; ++v) {
+      const float4 t = *(const float4 *)(g + q * G + 4 * v);
+      gv[4 * v] = t.x; gv[4 * v + 1] = t.y; gv[4 * v + 2] = t.z; gv[4 * v + 3] = t.w;
+    }
+    uint32_t ow[NW + 1];
+#pragma unroll
+    for (int k = 0; k <= NW; ++k) ow[k] = 0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int off = j * bits, k = off >> 5, sh = off & 31;
+      uint32_t c;
+      if constexpr (bits == 32) c = cw[k];
+      else c = (uint32_t)((((uint64_t)cw[k + 1] << 32) | cw[k]) >> sh) & mask;
+      const uint32_t nc = (uint32_t)fix_code<DT>(value(c, q * G + j, gv[j]), scale, minv) & mask;
+      ow[k] |= nc << sh;
+      if (sh + bits > 32) ow[k + 1] |= nc >> (32 - sh);
+    }
+    if constexpr (NW == 4) {
+      *(uint4 *)words = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NW; ++k) words[k] = ow[k];
+    }
+  }
+  if (blk == 0) {
+    constexpr int U = unit_elems<DT>();
+    const int64_t u = groups * (G / U) + threadIdx.x, units = (n + U - 1) / U;
+    if (u < units) sgd_unit<DT>(body, nullptr, n, g, lr, scale, minv, u);
+  }
+}
+
+// Threads the SGD of an n-element store of a packed format takes.
+template <int DT, bool WIDE = true>
+int64_t sgd_threads(int64_t n) {
+  if constexpr (WIDE && sgdw_group<DT>() > 0) return n / sgdw_group<DT>() + 1;
+  else return (n + unit_elems<DT>() - 1) / unit_elems<DT>();
+}
+
+// WIDE: the grouped path where the format has one (the gradient then must
+// be 16-byte aligned); else one unit per thread.
+template <int DT, bool WIDE>
 __global__ void __launch_bounds__(kThreads) sgd_kernel(uint8_t *__restrict__ body,
                                                        uint8_t *__restrict__ kbody, int64_t n,
                                                        const float *__restrict__ g, double lr,
                                                        float scale, float minv, int *stop,
                                                        const int *bad, int bad_value) {
   if (sgd_stopped(stop, bad, bad_value)) return;
-  sgd_units<DT>(body, kbody, n, g, lr, scale, minv, blockIdx.x, gridDim.x);
+  if constexpr (WIDE && sgdw_group<DT>() > 0) sgdw_units<DT>(body, n, g, lr, scale, minv, blockIdx.x, gridDim.x);
+  else sgd_units<DT>(body, kbody, n, g, lr, scale, minv, blockIdx.x, gridDim.x);
 }
 
 // sgd_kernel for the one-byte formats, 16 elements per thread: one 16-byte
@@ -407,18 +512,35 @@ __global__ void __launch_bounds__(kThreads) sgd_f64_kernel(double *__restrict__ 
 
 // welvet_sgd_f32_f64_grad welvet_dense.metal:263-281: the step is rounded to
 // f32 first, then subtracted in f32.
+// WIDE: four weights per thread (float4 loads and stores; w and g 16-byte
+// aligned), block 0 taking the n mod 4 tail; else one per thread.
+template <bool WIDE = true>
 __device__ inline void sgd_f32_units(float *__restrict__ w, int64_t n, const float *__restrict__ g, double lr,
                                      int64_t blk, int64_t nblk) {
-  for (int64_t i = blk * kThreads + threadIdx.x; i < n; i += nblk * kThreads) {
-    const float step = (float)(lr * (double)g[i]);
-    w[i] = w[i] - step;
+  auto step = [lr](float wi, float gi) { return wi - (float)(lr * (double)gi); };
+  if constexpr (!WIDE) {
+    for (int64_t i = blk * kThreads + threadIdx.x; i < n; i += nblk * kThreads) w[i] = step(w[i], g[i]);
+    return;
   }
+  const int64_t quads = n / 4;
+  for (int64_t q = blk * kThreads + threadIdx.x; q < quads; q += nblk * kThreads) {
+    float4 wv = *(const float4 *)(w + 4 * q);
+    const float4 gv = *(const float4 *)(g + 4 * q);
+    wv.x = step(wv.x, gv.x);
+    wv.y = step(wv.y, gv.y);
+    wv.z = step(wv.z, gv.z);
+    wv.w = step(wv.w, gv.w);
+    *(float4 *)(w + 4 * q) = wv;
+  }
+  const int64_t i = quads * 4 + threadIdx.x;
+  if (blk == 0 && i < n) w[i] = step(w[i], g[i]);
 }
+template <bool WIDE>
 __global__ void __launch_bounds__(kThreads) sgd_f32_kernel(float *__restrict__ w, int64_t n,
                                                            const float *__restrict__ g, double lr,
                                                            int *stop, const int *bad, int bad_value) {
   if (sgd_stopped(stop, bad, bad_value)) return;
-  sgd_f32_units(w, n, g, lr, blockIdx.x, gridDim.x);
+  sgd_f32_units<WIDE>(w, n, g, lr, blockIdx.x, gridDim.x);
 }
 
 // The SGD of up to kSgdBatch stores of one dtype in one launch (blockIdx.y =
@@ -454,6 +576,8 @@ __global__ void __launch_bounds__(kThreads) sgd_batch_kernel(SgdBatch b, double 
   else if constexpr (DT == kFloat64) sgd_f64_units((double *)t.body, t.n, t.g, lr, blockIdx.x, gridDim.x);
   else if constexpr (dtype_bits(DT) == 8 && fix_bytes<DT>() == 1)
     sgd8_units<DT, G>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x, t.nonfinite);
+  else if constexpr (sgdw_group<DT>() > 0)
+    sgdw_units<DT>(t.body, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x);
   else
     sgd_units<DT>(t.body, t.kbody, t.n, t.g, lr, t.scale, t.minv, blockIdx.x, gridDim.x);
 }
@@ -543,8 +667,15 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
                       float scale, float minv, int *stop, const int *bad, int bad_value, hipStream_t s,
                       int *nonfinite) {
   if ((dt == kFP8E4M3 || dt == kFP8E5M2) && kbody == nullptr) return hipErrorInvalidValue;
+  // the grouped kernels read the gradient as float4; a gradient at another
+  // alignment (a slice of a concatenated buffer) takes one element or unit
+  // per thread
+  const bool wide = ((uintptr_t)g & 15) == 0;
   if (dt == kFloat32) {
-    sgd_f32_kernel<<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop, bad, bad_value);
+    if (wide)
+      sgd_f32_kernel<true><<<grid_for(n / 4 + 1), kThreads, 0, s>>>((float *)body, n, g, lr, stop, bad, bad_value);
+    else
+      sgd_f32_kernel<false><<<grid_for(n), kThreads, 0, s>>>((float *)body, n, g, lr, stop, bad, bad_value);
     return hipGetLastError();
   }
   if (dt == kFloat64) {
@@ -553,7 +684,12 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
   }
 #define WH_SGD(D)                                                                           \
   if constexpr (dtype_bits(D) == 8 && fix_bytes<D>() == 1) {                               \
-    if (n >= ((int64_t)4 << 20))                                                            \
+    if (!wide) {                                                                            \
+      sgd_kernel<D, false><<<grid_for(n), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, stop, \
+                                                            bad, bad_value);                \
+      if (D == kFP8E5M2 && nonfinite != nullptr) /* every code was rewritten */             \
+        e5m2_nonfinite_kernel<<<grid_for(n / 16 + 1), kThreads, 0, s>>>(kbody, n, nonfinite); \
+    } else if (n >= ((int64_t)4 << 20))                                                     \
       sgd8_kernel<D, 16><<<grid_for(n / 16 + 1), kThreads, 0, s>>>(body, kbody, n, g, lr, scale, minv, \
                                                                   stop, bad, bad_value, nonfinite); \
     else /* small stores: four codes per thread, four times the threads */                \
@@ -561,8 +697,12 @@ hipError_t launch_sgd(int dt, uint8_t *body, uint8_t *kbody, int64_t n, const fl
                                                                 stop, bad, bad_value, nonfinite); \
     return hipGetLastError();                                                               \
   } else if constexpr (D != kFloat32 && D != kFloat64) {                                    \
-    sgd_kernel<D><<<grid_for((n + unit_elems<D>() - 1) / unit_elems<D>()), kThreads, 0, s>>>( \
-        body, kbody, n, g, lr, scale, minv, stop, bad, bad_value);                          \
+    if (wide)                                                                               \
+      sgd_kernel<D, true><<<grid_for(sgd_threads<D>(n)), kThreads, 0, s>>>(                 \
+          body, kbody, n, g, lr, scale, minv, stop, bad, bad_value);                        \
+    else                                                                                    \
+      sgd_kernel<D, false><<<grid_for(sgd_threads<D, false>(n)), kThreads, 0, s>>>(         \
+          body, kbody, n, g, lr, scale, minv, stop, bad, bad_value);                        \
     return hipGetLastError();                                                               \
   } else {                                                                                  \
     return hipErrorInvalidValue;                                                            \
@@ -582,6 +722,7 @@ hipError_t launch_sgd_batch(int dt, const SgdBatch &b, double lr, int *stop, con
   int64_t maxn = 0;
   for (int i = 0; i < b.count; ++i) {
     if (b.store[i].body == nullptr || b.store[i].g == nullptr || b.store[i].n < 0) return hipErrorInvalidValue;
+    if (((uintptr_t)b.store[i].g & 15) != 0) return hipErrorInvalidValue;  // read as float4
     if ((dt == kFP8E4M3 || dt == kFP8E5M2) && b.store[i].kbody == nullptr) return hipErrorInvalidValue;
     maxn = std::max(maxn, b.store[i].n);
   }
@@ -592,7 +733,7 @@ hipError_t launch_sgd_batch(int dt, const SgdBatch &b, double lr, int *stop, con
     else                                                                                            \
       sgd_batch_kernel<D, 4><<<dim3(grid_for(maxn / 4 + 1), b.count), kThreads, 0, s>>>(b, lr, stop, bad, first);   \
   } else {                                                                                          \
-    const int64_t units = (D == kFloat32 || D == kFloat64) ? maxn : (maxn + unit_elems<D>() - 1) / unit_elems<D>(); \
+    const int64_t units = D == kFloat32 ? maxn / 4 + 1 : D == kFloat64 ? maxn : sgd_threads<D>(maxn); \
     sgd_batch_kernel<D, 4><<<dim3(grid_for(units), b.count), kThreads, 0, s>>>(b, lr, stop, bad, first); \
   }                                                                                                 \
   return hipGetLastError();
