@@ -335,9 +335,13 @@ __device__ __forceinline__ void sgdw_units(uint8_t *__restrict__ body, int64_t n
                 "whole words and units per group");
   constexpr uint32_t mask = bits >= 32 ? ~0u : (1u << bits) - 1;
   constexpr bool kTab = DT == kFP4 || DT == kNF4;
+  // FP4 / NF4: the decoded values and the windowed search in LDS
   __shared__ float tab[kTab ? 16 : 1];
+  __shared__ __align__(16) TabSearch search_s[1];
   if constexpr (kTab) {
+    const uint32_t *from = (const uint32_t *)(DT == kNF4 ? &kNf4Search : &kFp4Search);
     if (threadIdx.x < 16) tab[threadIdx.x] = dec_code<DT>(threadIdx.x, scale, minv);
+    for (int i = threadIdx.x; i < (int)(sizeof(TabSearch) / 4); i += kThreads) ((uint32_t *)search_s)[i] = from[i];
     __syncthreads();
   }
   auto value = [&](uint32_t c, int64_t i, float gj) {
@@ -348,6 +352,12 @@ __device__ __forceinline__ void sgdw_units(uint8_t *__restrict__ body, int64_t n
     } else {
       return sgd_value<DT>(c, i, gj, lr, scale, minv);
     }
+  };
+  // fix_code<DT> (the NF4 / FP4 search through the window)
+  auto code_of = [&](float v) -> uint32_t {
+    if constexpr (DT == kNF4) return nearest_window<true>(search_s[0], v / (scale == 0.0f ? 1.0f : scale));
+    else if constexpr (DT == kFP4) return nearest_window<false>(search_s[0], v);
+    else return (uint32_t)fix_code<DT>(v, scale, minv);
   };
   const int64_t groups = n / G;
   for (int64_t q = blk * kThreads + threadIdx.x; q < groups; q += nblk * kThreads) {
@@ -376,7 +386,7 @@ __device__ __forceinline__ void sgdw_units(uint8_t *__restrict__ body, int64_t n
       uint32_t c;
       if constexpr (bits == 32) c = cw[k];
       else c = (uint32_t)((((uint64_t)cw[k + 1] << 32) | cw[k]) >> sh) & mask;
-      const uint32_t nc = (uint32_t)fix_code<DT>(value(c, q * G + j, gv[j]), scale, minv) & mask;
+      const uint32_t nc = code_of(value(c, q * G + j, gv[j])) & mask;
       ow[k] |= nc << sh;
       if (sh + bits > 32) ow[k + 1] |= nc >> (32 - sh);
     }

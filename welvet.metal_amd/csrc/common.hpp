@@ -195,17 +195,18 @@ __device__ inline float dec_e5m2(uint32_t b) {
 }
 
 // float_codecs.cpp:184 and native_codec.cpp:93-110 as bit patterns
-__device__ __constant__ const float kFp4Tab[16] = {0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f,
-                                                   -0.f, -.5f, -1.f, -1.5f, -2.f, -3.f, -4.f, -6.f};
-__device__ __constant__ const float kNf4Tab[16] = {
-    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
-    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
-    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
-    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+#define WH_FP4_VALUES 0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f, -0.f, -.5f, -1.f, -1.5f, -2.f, -3.f, -4.f, -6.f
+#define WH_NF4_VALUES                                                                            \
+  -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f, -0.28444138169288635f, \
+      -0.18477343022823334f, -0.09105003625154495f, 0.0f, 0.07958029955625534f, 0.16093020141124725f, \
+      0.24611230194568634f, 0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,       \
+      0.7229568362236023f, 1.0f
+__device__ __constant__ const float kFp4Tab[16] = {WH_FP4_VALUES};
+__device__ __constant__ const float kNf4Tab[16] = {WH_NF4_VALUES};
 
 // Nearest table entry, first index wins ties, NaN/Inf -> 0
 // (float_codecs.cpp:187-198, native_codec.cpp:525-534).
-__device__ inline uint32_t nearest16(const float *tab, float r) {
+__host__ __device__ inline uint32_t nearest16(const float *tab, float r) {
   uint32_t best = 0;
   float best_err = 3.402823466e38f;
 #pragma unroll
@@ -213,6 +214,66 @@ __device__ inline uint32_t nearest16(const float *tab, float r) {
     const float e = fabsf(r - tab[c]);
     if (e < best_err) { best_err = e; best = (uint32_t)c; }
   }
+  return best;
+}
+
+// nearest16 for FP4 and NF4 through a window of four candidates.  The NF4
+// values are sorted; FP4 is searched on |r| over its eight magnitudes (code k
+// for r >= 0, k + 8 for r < 0 and k > 0: the +0 code 0 ties the -0 code 8 at
+// every r and wins on its index; a code of the other sign is never nearer).
+// A bucket of r (1/16 wide over [-2, 2] for NF4, 1/4 over [0, 8] for the FP4
+// magnitude) gives the window's first index: one before the last entry at or
+// below the bucket's start, so a bucket misjudged by one rounding still holds
+// the answer.  Within |r| <= 2 (NF4) or 64 (FP4) the f32 errors of entries
+// outside the window are strictly larger (entries >= 0.079 apart, far above
+// an ulp of the error), so the window's first-index minimum is nearest16's;
+// elsewhere, and for NaN, the full search runs.  Checked against nearest16 on
+// every f32 of both ranges (tests/native/nearest_check.cpp).
+struct TabSearch {
+  float val[16];      // nearest16's table (code order)
+  float win[13][4];   // sorted values (NF4) / magnitudes (FP4) k0 .. k0 + 3
+  uint8_t first[64];  // bucket -> k0
+};
+template <bool NF4>
+__host__ __device__ constexpr TabSearch make_tab_search() {
+  TabSearch t{};
+  const float fp4[16] = {WH_FP4_VALUES}, nf4[16] = {WH_NF4_VALUES};
+  float sorted[16] = {};
+  const int n = NF4 ? 16 : 8, nb = NF4 ? 64 : 32, last = n - 4;
+  for (int i = 0; i < 16; ++i) t.val[i] = NF4 ? nf4[i] : fp4[i];
+  for (int i = 0; i < n; ++i) sorted[i] = NF4 ? nf4[i] : fp4[i];  // FP4 codes 0-7: the magnitudes
+  for (int k = 0; k <= last; ++k)
+    for (int j = 0; j < 4; ++j) t.win[k][j] = sorted[k + j];
+  for (int b = 0; b < nb; ++b) {
+    const float start = NF4 ? (float)b / 16.0f - 2.0f : (float)b / 4.0f;
+    int lo = 0;
+    for (int k = 0; k < n; ++k)
+      if (sorted[k] <= start) lo = k;
+    const int k0 = lo - 1 < 0 ? 0 : (lo - 1 > last ? last : lo - 1);
+    t.first[b] = (uint8_t)k0;
+  }
+  return t;
+}
+__device__ __constant__ const TabSearch kFp4Search = make_tab_search<false>();
+__device__ __constant__ const TabSearch kNf4Search = make_tab_search<true>();
+// t: make_tab_search<NF4>() (a copy in LDS on the device)
+template <bool NF4>
+__host__ __device__ inline uint32_t nearest_window(const TabSearch &t, float r) {
+  const float m = NF4 ? r : fabsf(r);
+  if (!(fabsf(r) <= (NF4 ? 2.0f : 64.0f))) return nearest16(t.val, r);
+  int b = NF4 ? (int)((r + 2.0f) * 16.0f) : (int)(m * 4.0f);
+  const int nb = NF4 ? 64 : 32;
+  b = b < 0 ? 0 : (b >= nb ? nb - 1 : b);
+  const int k0 = t.first[b];
+  const float *w = t.win[k0];
+  uint32_t best = (uint32_t)k0;
+  float be = fabsf(m - w[0]);
+#pragma unroll
+  for (int j = 1; j < 4; ++j) {
+    const float e = fabsf(m - w[j]);
+    if (e < be) { be = e; best = (uint32_t)(k0 + j); }
+  }
+  if (!NF4 && best > 0 && r < 0.0f) best += 8;
   return best;
 }
 
