@@ -542,7 +542,8 @@ def run_configs(torch, P, only=("c1", "c2", "c3", "c4", "c5"), cpu=True, c5_dtyp
             torch, P, (1, 1, 2, 1), [2048, 8192, 2048], dt, 256, 10, seed + 3)
     c5, skipped = {}, []
     for dt in c5_dtypes if "c5" in only else ():
-        r = time_volume_train(torch, P, (2, 2, 2, 4), [1024] * 33, dt, 16, 2, seed + 4)
+        # 10 timed steps per dtype (about 5 ms; mounting the 32 stores dominates the leg)
+        r = time_volume_train(torch, P, (2, 2, 2, 4), [1024] * 33, dt, 16, 10, seed + 4)
         c5[P.DTYPE_NAMES[dt]] = round(r["ms_per_step"], 4)
         if r["sgd_skipped_nonfinite"]:
             skipped.append(P.DTYPE_NAMES[dt])
