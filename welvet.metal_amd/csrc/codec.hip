@@ -254,9 +254,6 @@ __device__ inline bool sgd_stopped(int *stop, const int *bad, int bad_value) {
   return stop != nullptr && *stop != 0;
 }
 
-// The SGD element loops below take their block index and block count as
-// arguments: one launch per store (the block grid) or one launch for several
-// stores (sgd_batch_kernel: blockIdx.y picks the store).
 // The SGD of unit u (unit_elems elements, so no two threads touch a byte).
 template <int DT>
 __device__ inline void sgd_unit(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
@@ -296,6 +293,9 @@ __device__ inline void sgd_unit(uint8_t *__restrict__ body, uint8_t *__restrict_
   }
 }
 
+// The SGD element loops below take their block index and block count as
+// arguments: one launch per store (the block grid) or one launch for several
+// stores (sgd_batch_kernel: blockIdx.y picks the store).
 template <int DT>
 __device__ inline void sgd_units(uint8_t *__restrict__ body, uint8_t *__restrict__ kbody, int64_t n,
                                  const float *__restrict__ g, double lr, float scale, float minv,
@@ -329,7 +329,7 @@ __host__ __device__ constexpr int sgdw_group() {
 // flight); every thread of the block must call this.
 template <int DT>
 __device__ __forceinline__ void sgdw_units(uint8_t *__restrict__ body, int64_t n, const float *__restrict__ g,
-                                  double lr, float scale, float minv, int64_t blk, int64_t nblk) {
+                                           double lr, float scale, float minv, int64_t blk, int64_t nblk) {
   constexpr int bits = dtype_bits(DT), G = sgdw_group<DT>(), NW = G * bits / 32;
   static_assert(G > 0 && G % 4 == 0 && G * bits % 32 == 0 && G % unit_elems<DT>() == 0,
                 "whole words and units per group");
